@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""bench.py -- Q4_0 decode-GEMV throughput on one MI355X.
+
+A "step" is one pass of the Llama-3-8B per-layer decode GEMV set at batch 1
+(Wq 4096x4096, Wk/Wv 1024x4096, Wo 4096x4096, W_gate/W_up 14336x4096,
+W_down 4096x14336; Q4_0 weights, fp32 activations ~ N(0,1)), executed as the
+decode step runs it: the input digits are prepared once per input vector,
+Q|K|V run as one fused launch, W_gate|W_up as one, Wo and W_down alone.
+Each step is replayed from a captured HIP graph and uses the next of
+LAYERS distinct weight sets (4 x 136.6 MB), so the 256 MB MALL cannot serve
+repeats.  Inputs are resident in HBM when the timed region starts.
+
+value  = algorithmic bytes of the K timed steps / wall time of those steps,
+         algorithmic bytes per step = sum over the 7 matrices of
+         (weights + 4*N + 4*M) = 136,642,560 B.
+roofline = the dominant kernel (the fused W_gate|W_up GEMV launch), timed
+         with HIP events on its stream over K eager launches: achieved =
+         its algorithmic bytes / mean launch duration, vs 8 TB/s.
+cpu_baseline = the reference's own q_gemv_q4_f32_avx2 (compiled from its
+         sources into oracle/_ref) running the same 7-matrix set on one
+         pinned host core of this machine, for a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "project-ia_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "Q4_0 GEMV HBM GB/s (% peak) + decode tok/s, Llama-3-8B shape, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+DIM, KV, HID = 4096, 1024, 14336
+SHAPES = [("wq", DIM, DIM), ("wk", KV, DIM), ("wv", KV, DIM), ("wo", DIM, DIM),
+          ("w_gate", HID, DIM), ("w_up", HID, DIM), ("w_down", DIM, HID)]
+LAYERS = 4
+
+
+def alg_bytes(M, N):
+    return M * (N // 32) * 20 + 4 * N + 4 * M
+
+
+STEP_BYTES = sum(alg_bytes(M, N) for _, M, N in SHAPES)
+GATE_UP_BYTES = alg_bytes(HID, DIM) * 2
+assert STEP_BYTES == 136_642_560
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class LayerSet:
+    """Device-resident weights of one layer + tensor views."""
+
+    def __init__(self, qa, mats):
+        self.bufs = {k: qa.DeviceBuffer.from_numpy(w) for k, w in mats.items()}
+        self.t = {k: qa.q4_tensor(self.bufs[k].ptr, M, N) for k, M, N in SHAPES}
+
+
+def gen_layer(seed):
+    from oracle import oracle as orc
+    rng = orc.rng_for(seed)
+    return {k: orc.gen_q4(M, N, rng) for k, M, N in SHAPES}
+
+
+def ptr_array(ptrs, ctype=C.c_void_p):
+    return (ctype * len(ptrs))(*ptrs)
+
+
+def run_gpu(args):
+    import qorus_amd as qa
+    from oracle import oracle as orc
+    lib = qa.lib()
+    if not qa.gpu_available():
+        raise SystemExit("bench.py: no usable GPU (" + lib.qh_last_error().decode() + ")")
+    log(f"[bench] device {lib.qh_arch_name().decode()}; generating {LAYERS} layers "
+        f"({LAYERS * STEP_BYTES / 1e6:.0f} MB)")
+    layers = [LayerSet(qa, gen_layer(1000 + l)) for l in range(LAYERS)]
+    rng = orc.rng_for(77)
+    xin = {k: qa.DeviceBuffer.from_numpy(orc.gen_f32(n, rng)) for k, n in
+           (("h", DIM), ("o", DIM), ("h2", DIM), ("m", HID))}
+    outs = {k: qa.DeviceBuffer(M * 4) for k, M, _ in SHAPES}
+    ws = {k: qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(n)) for k, n in
+          (("h", DIM), ("o", DIM), ("h2", DIM), ("m", HID))}
+    stream = qa.Stream()
+    s = stream.handle
+
+    def enqueue_step(L, prepared_only=False):
+        """The 4 prepare + 4 GEMV launches of one layer pass."""
+        groups = [("h", ["wq", "wk", "wv"]), ("o", ["wo"]), ("h2", ["w_gate", "w_up"]), ("m", ["w_down"])]
+        for xk, mats in groups:
+            if not prepared_only:
+                qa.check(lib.qh_gemv_prepare(xin[xk].ptr, DIM if xk != "m" else HID, ws[xk].ptr, s), "prepare")
+            Ws = ptr_array([L.t[m].addr for m in mats])
+            ys = ptr_array([outs[m].ptr for m in mats])
+            qa.check(lib.qh_gemv_q4_f32_prepared(Ws, None, ys, len(mats), ws[xk].ptr, s), "gemv")
+
+    # One captured graph per layer.
+    graphs = []
+    for L in layers:
+        qa.check(lib.qh_stream_begin_capture(s), "begin_capture")
+        enqueue_step(L)
+        g = C.c_void_p()
+        qa.check(lib.qh_stream_end_capture(s, C.byref(g)), "end_capture")
+        graphs.append(g.value)
+
+    for i in range(args.warmup):
+        qa.check(lib.qh_graph_launch(graphs[i % LAYERS], s))
+    stream.sync()
+
+    # ---- timed region: exactly K steps, synchronized on both sides ----
+    qa.check(lib.qh_device_synchronize())
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        qa.check(lib.qh_graph_launch(graphs[i % LAYERS], s))
+    stream.sync()
+    qa.check(lib.qh_device_synchronize())
+    t1 = time.perf_counter()
+    wall = t1 - t0
+
+    # ---- dominant kernel: fused gate|up GEMV, HIP events on its stream ----
+    for k in ("h", "o", "h2", "m"):
+        qa.check(lib.qh_gemv_prepare(xin[k].ptr, DIM if k != "m" else HID, ws[k].ptr, s))
+    ev = [(qa.Event(), qa.Event()) for _ in range(args.steps)]
+    per_kernel = {"qkv": [], "wo": [], "gate_up": [], "down": []}
+    evk = [[(qa.Event(), qa.Event()) for _ in range(4)] for _ in range(min(args.steps, 64))]
+    stream.sync()
+    for i in range(args.steps):
+        L = layers[i % LAYERS]
+        Ws = ptr_array([L.t["w_gate"].addr, L.t["w_up"].addr])
+        ys = ptr_array([outs["w_gate"].ptr, outs["w_up"].ptr])
+        ev[i][0].record(stream)
+        qa.check(lib.qh_gemv_q4_f32_prepared(Ws, None, ys, 2, ws["h2"].ptr, s))
+        ev[i][1].record(stream)
+    stream.sync()
+    dur_ms = [a.elapsed_ms(b) for a, b in ev]
+    # per-kernel breakdown of one layer pass (eager, events between launches)
+    groups = [("qkv", "h", ["wq", "wk", "wv"]), ("wo", "o", ["wo"]), ("gate_up", "h2", ["w_gate", "w_up"]),
+              ("down", "m", ["w_down"])]
+    for i, pairs in enumerate(evk):
+        L = layers[i % LAYERS]
+        for (name, xk, mats), (a, b) in zip(groups, pairs):
+            Ws = ptr_array([L.t[m].addr for m in mats])
+            ys = ptr_array([outs[m].ptr for m in mats])
+            a.record(stream)
+            qa.check(lib.qh_gemv_q4_f32_prepared(Ws, None, ys, len(mats), ws[xk].ptr, s))
+            b.record(stream)
+    stream.sync()
+    for pairs in evk:
+        for (name, _, _), (a, b) in zip(groups, pairs):
+            per_kernel[name].append(a.elapsed_ms(b))
+    kbytes = {"qkv": sum(alg_bytes(M, N) for k, M, N in SHAPES if k in ("wq", "wk", "wv")),
+              "wo": alg_bytes(DIM, DIM), "gate_up": GATE_UP_BYTES, "down": alg_bytes(DIM, HID)}
+    breakdown = {}
+    for name, v in per_kernel.items():
+        us = float(np.mean(v)) * 1e3
+        breakdown[name] = {"us": round(us, 2), "GB_s": round(kbytes[name] / (us * 1e-6) / 1e9, 1)}
+    for g in graphs:
+        lib.qh_graph_destroy(g)
+    mean_ms = float(np.mean(dur_ms))
+    achieved = GATE_UP_BYTES / (mean_ms * 1e-3) / 1e9
+    return wall, achieved, mean_ms, breakdown
+
+
+def run_cpu_baseline(seconds):
+    """Reference q_gemv_q4_f32_avx2 (oracle/_ref) on one pinned core."""
+    from oracle import oracle as orc
+    kind = "reference" if orc.ref_available() else "port"
+    mats = gen_layer(1000)
+    rng = orc.rng_for(78)
+    xs = {DIM: orc.aligned_copy(orc.gen_f32(DIM, rng)), HID: orc.aligned_copy(orc.gen_f32(HID, rng))}
+    ys = {k: orc.aligned_empty((M,), np.float32) for k, M, _ in SHAPES}
+    Wa = {k: orc.aligned_copy(mats[k].reshape(-1)) for k, _, _ in SHAPES}
+    tens = {k: orc.q4_tensor(Wa[k].ctypes.data, M, N) for k, M, N in SHAPES}
+    if kind == "reference":
+        fn = orc.ref().q_gemv_q4_f32_avx2
+
+        def one_pass():
+            for k, M, N in SHAPES:
+                rc = fn(C.addressof(tens[k][0]), xs[N].ctypes.data, ys[k].ctypes.data)
+                assert rc == 0
+    else:
+        L = orc.lib()
+
+        def one_pass():
+            for k, M, N in SHAPES:
+                L.or_gemv_q4(Wa[k], M, N, xs[N], ys[k])
+    try:
+        old = os.sched_getaffinity(0)
+        core = min(old)
+        os.sched_setaffinity(0, {core})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        one_pass()  # warm-up
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            one_pass()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 1000:
+                break
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    gbs = n * STEP_BYTES / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{n} passes of the config-2 per-layer Q4_0 GEMV set ({STEP_BYTES / 1e6:.1f} MB/pass) "
+                      f"in {el:.1f} s on 1 pinned core ({orc.cpu_model_name()})"}
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (profiles/gemv_gate_up_traffic.json), or None."""
+    p = REPO / "profiles" / "gemv_gate_up_traffic.json"
+    try:
+        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (batch-1 decode of an 8B model is not "
+              f"sharded); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    wall, achieved, kern_ms, breakdown = run_gpu(args)
+    ms_per_step = wall / args.steps * 1e3
+    value = STEP_BYTES * args.steps / wall / 1e9
+    cpu = None if args.no_cpu else run_cpu_baseline(args.cpu_seconds)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 x f32 (int4 digit-plane dot, f32 scale/accumulate)",
+        "data": "synthetic (seeded: nibbles U{0..15}, scale |N(0,1)|*0.02, x ~ N(0,1))",
+        "config": {"workload": "config2: Llama-3-8B per-layer decode GEMV set at batch 1 "
+                               "(Wq,Wk,Wv,Wo,W_gate,W_up,W_down Q4_0; fp32 x)",
+                   "layers_rotated": LAYERS, "bytes_per_step": STEP_BYTES,
+                   "launches_per_step": 8, "step_exec": "hipGraph replay"},
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "k_gemv (fused W_gate|W_up, 28672x4096)",
+                     "alg_bytes_per_launch": GATE_UP_BYTES, "mean_launch_us": round(kern_ms * 1e3, 2)},
+        "kernels": breakdown,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

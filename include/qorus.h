@@ -1,0 +1,109 @@
+/*
+ * qorus.h -- public C API of the Qorus-IA quantized matrix path, implemented
+ * for AMD Instinct MI355X (gfx950) by libqorus_hip.so.
+ *
+ * Every entry point keeps the name, signature, argument meaning, validation
+ * order and q_error_code returns of the reference declaration it replaces
+ * (cited per function), so existing callers relink unchanged.  The op entry
+ * points take HOST pointers and are synchronous, exactly like the reference:
+ * inputs are copied to HBM, the gfx950 kernel runs, outputs are copied back.
+ * Q4_0 views whose data lie inside a model mapped by q_init_memory[_ex] are
+ * read from the HBM-resident copy made at load time, with no per-call copy.
+ * The stream-ordered device entry points used by the on-device decode step
+ * are declared in qorus_hip.h.
+ *
+ * Out of scope for this build (declared nowhere, so a caller fails at link
+ * time rather than at run time): the BPE tokenizer (reference qorus.h:230-273)
+ * and q_generate (reference qorus.h:318-320).
+ */
+#ifndef QORUS_H
+#define QORUS_H
+
+#include "qorus_types.h"
+
+#ifdef __cplusplus
+#define Q_RESTRICT __restrict__
+extern "C" {
+#else
+#define Q_RESTRICT restrict
+#endif
+
+/* ---- Memory tiers (reference include/qorus.h:16-39, src/core/memory.c) ---- */
+
+/* Map a .qorus file (tier 1) and upload it once to HBM.
+ * Replaces reference qorus.h:16 / memory.c:131-133. */
+q_error_code q_init_memory(q_context* Q_RESTRICT ctx, const char* model_path);
+
+/* As q_init_memory with an explicit host mapping strategy.
+ * Replaces reference qorus.h:21 / memory.c:60-128. */
+q_error_code q_init_memory_ex(q_context* Q_RESTRICT ctx, const char* model_path,
+                              q_mmap_strategy strategy);
+
+/* Allocate the tier-2 KV cache, zero-filled, in HBM (kv_buffer is a device
+ * address).  Replaces reference qorus.h:25 / memory.c:136-164. */
+q_error_code q_alloc_kv_cache(q_context* Q_RESTRICT ctx, size_t kv_size);
+
+/* Allocate the tier-3 host arena (tensor views, model structs).
+ * Replaces reference qorus.h:29 / memory.c:168-195. */
+q_error_code q_alloc_arena(q_context* Q_RESTRICT ctx, size_t arena_size);
+
+/* 64-byte aligned bump allocation; NULL on OOM.
+ * Replaces reference qorus.h:33 / memory.c:199-259. */
+void* q_arena_alloc(q_context* Q_RESTRICT ctx, size_t size);
+
+/* Rewind the arena to the model watermark.
+ * Replaces reference qorus.h:36 / memory.c:265-315. */
+void q_arena_reset(q_context* Q_RESTRICT ctx);
+
+/* Release arena, KV cache, HBM mirrors and mapping (LIFO).
+ * Replaces reference qorus.h:39 / memory.c:317-355. */
+void q_free_memory(q_context* Q_RESTRICT ctx);
+
+/* Replaces reference qorus.h:47 / src/core/utils.c:11-31. */
+const char* q_strerror(q_error_code err);
+
+/* ---- Ops (host pointers, synchronous) ---- */
+
+/* Dequantize one Q4_0 block into 32 floats; silent no-op on NULL.
+ * Replaces reference qorus.h:58-61 / src/ops/avx2/dequantize.c:82-96. */
+void q_dequantize_q4_0_block_avx2_public(const q_block_q4_0* Q_RESTRICT block,
+                                         float* Q_RESTRICT output);
+
+/* y[M] = W[M x N] . x[N] with Q4_0 W.
+ * Replaces reference qorus.h:70-74 / src/ops/avx2/matmul.c:98-271. */
+q_error_code q_gemv_q4_f32_avx2(const q_tensor* Q_RESTRICT weights,
+                                const float* Q_RESTRICT input,
+                                float* Q_RESTRICT output);
+
+/* out = a + b (1-D, in-place allowed).
+ * Replaces reference qorus.h:109-113 / src/ops/avx2/add_fp32.c:17-164. */
+q_error_code q_add_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output);
+
+/* out = a * b (1-D, in-place allowed).
+ * Replaces reference qorus.h:122-126 / src/ops/avx2/mul_fp32.c:17-126. */
+q_error_code q_mul_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output);
+
+/* y = x * rsqrt(mean(x^2) + eps) * weight.
+ * Replaces reference qorus.h:138-144 / src/ops/avx2/rmsnorm.c:15-92. */
+q_error_code q_rmsnorm_f32_avx2(const float* Q_RESTRICT x, const float* Q_RESTRICT weight,
+                                float* Q_RESTRICT output, uint32_t N, float eps);
+
+/* Interleaved-pair rotation with duplicated cos/sin tables [c0,c0,c1,c1,...].
+ * Replaces reference qorus.h:153-159 / src/ops/avx2/rope.c:23-110. */
+q_error_code q_rope_f32_avx2(const float* Q_RESTRICT x, const float* Q_RESTRICT cos,
+                             const float* Q_RESTRICT sin, float* Q_RESTRICT output,
+                             uint32_t N);
+
+/* y = x * sigmoid(x) with the reference's polynomial exp.
+ * Replaces reference qorus.h:167-171 / src/ops/avx2/silu.c:18-94. */
+q_error_code q_silu_f32_avx2(const float* Q_RESTRICT x, float* Q_RESTRICT output, uint32_t N);
+
+/* Max-shifted softmax with the reference's polynomial exp.
+ * Replaces reference qorus.h:179-183 / src/ops/avx2/softmax.c:17-132. */
+q_error_code q_softmax_f32_avx2(const float* Q_RESTRICT x, float* Q_RESTRICT output, uint32_t N);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QORUS_H */

@@ -1,0 +1,126 @@
+/*
+ * qorus_hip.h -- stream-ordered DEVICE entry points of libqorus_hip.so.
+ *
+ * These are the MI355X-native counterparts of the qorus.h ops: every pointer
+ * argument is a device (HBM) address, every call is asynchronous on the given
+ * stream (NULL = the null stream) and returns after validating its arguments
+ * and enqueuing its kernels.  Validation order and q_error_code values follow
+ * the reference op each entry point mirrors (cited per function); a kernel
+ * launch failure is reported as Q_ERR_INVALID_ARG with the HIP message
+ * available from qh_last_error().
+ *
+ * No CPU fallback exists: with no usable gfx950 device every entry point
+ * returns Q_ERR_ALLOC_FAILED.
+ */
+#ifndef QORUS_HIP_H
+#define QORUS_HIP_H
+
+#include "qorus_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* qh_stream; /* a hipStream_t */
+typedef void* qh_event;  /* a hipEvent_t */
+
+/* ---- Runtime plumbing (no reference counterpart: the reference is CPU-only) ---- */
+
+/* 1 if a GPU is visible and the library's device state initialised. */
+int qh_available(void);
+/* Text of the last HIP failure seen by the library ("" if none). */
+const char* qh_last_error(void);
+/* gfx architecture name of the current device, e.g. "gfx950". */
+const char* qh_arch_name(void);
+
+q_error_code qh_malloc(void** ptr, size_t bytes);
+q_error_code qh_free(void* ptr);
+/* Synchronous copies (host memory may be pageable). */
+q_error_code qh_memcpy_htod(void* dst, const void* src, size_t bytes);
+q_error_code qh_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+q_error_code qh_memcpy_dtod(void* dst, const void* src, size_t bytes, qh_stream s);
+q_error_code qh_memset(void* dst, int value, size_t bytes, qh_stream s);
+q_error_code qh_stream_create(qh_stream* s);
+q_error_code qh_stream_destroy(qh_stream s);
+q_error_code qh_stream_synchronize(qh_stream s);
+q_error_code qh_device_synchronize(void);
+q_error_code qh_event_create(qh_event* e);
+q_error_code qh_event_destroy(qh_event e);
+q_error_code qh_event_record(qh_event e, qh_stream s);
+q_error_code qh_event_synchronize(qh_event e);
+q_error_code qh_event_elapsed_ms(qh_event start, qh_event stop, float* ms);
+
+/* HIP graphs: capture the work enqueued on stream s between begin and end
+ * (by this thread) into an executable graph, then replay it. */
+typedef void* qh_graph; /* a hipGraphExec_t */
+q_error_code qh_stream_begin_capture(qh_stream s);
+q_error_code qh_stream_end_capture(qh_stream s, qh_graph* out);
+q_error_code qh_graph_launch(qh_graph g, qh_stream s);
+q_error_code qh_graph_destroy(qh_graph g);
+
+/* ---- Q4_0 dequantization and GEMV ---- */
+
+/* out[32*b + e] = fmaf(q_e, s_b, -8*s_b) for b < n_blocks (bit-exact with
+ * reference src/ops/avx2/dequantize.c:18-73).  out must be 16-byte aligned. */
+q_error_code qh_dequantize_q4_0(const void* blocks, float* out, uint64_t n_blocks, qh_stream s);
+
+/* Bytes of workspace qh_gemv_q4_f32 needs for an input of length N. */
+size_t qh_gemv_workspace_bytes(uint32_t N);
+
+/* y[M] = W[M x N] . x[N], W->data in HBM (AoS 20-byte Q4_0 blocks, 4-byte
+ * aligned), x/y 32-byte aligned.  Validation order and codes of reference
+ * src/ops/avx2/matmul.c:104-197, plus Q_ERR_MISALIGNED for a W->data that
+ * is not 4-byte aligned.  `workspace` holds >= qh_gemv_workspace_bytes(N)
+ * device bytes; NULL selects a library-owned per-device buffer (calls that
+ * overlap on one device then race on it).  Result: within 1e-5 of the fp64
+ * dot product, relative to sum_j |W_ij x_j|. */
+q_error_code qh_gemv_q4_f32(const q_tensor* W, const float* x, float* y, void* workspace,
+                            qh_stream s);
+
+/* y = W . x + residual (residual added last, as reference model.c:1620). */
+q_error_code qh_gemv_q4_f32_add(const q_tensor* W, const float* x, const float* residual,
+                                float* y, void* workspace, qh_stream s);
+
+/* Split form of the GEMV for inputs shared by several matrices (fused Q|K|V
+ * or gate|up in the decode step; no reference counterpart, the reference
+ * calls q_gemv_q4_f32_avx2 once per matrix, model.c:1120-1165).
+ * qh_gemv_prepare converts x (N floats, 32-byte aligned) into the integer
+ * digit planes the kernel consumes, in `workspace`; qh_gemv_q4_f32_prepared
+ * then computes ys[i] = Ws[i] . x (+ residuals[i] when residuals and
+ * residuals[i] are non-NULL) for 1 <= n <= 4 matrices with the same N, in
+ * one launch.  Each Ws[i] is validated as in qh_gemv_q4_f32. */
+q_error_code qh_gemv_prepare(const float* x, uint32_t N, void* workspace, qh_stream s);
+q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* const* residuals,
+                                     float* const* ys, uint32_t n, const void* workspace,
+                                     qh_stream s);
+
+/* ---- Vector ops (device pointers, same validation as the qorus.h op) ---- */
+
+/* Reference src/ops/avx2/rmsnorm.c:15-92 (sum of squares reduced as a fixed
+ * tree; the reference's 8-lane sequential order and rsqrtps seed are not
+ * reproduced bit-for-bit). */
+q_error_code qh_rmsnorm_f32(const float* x, const float* weight, float* output, uint32_t N,
+                            float eps, qh_stream s);
+/* Reference src/ops/avx2/rope.c:23-110 applied to n_vec consecutive vectors
+ * of length N (e.g. all heads of a token) with one table pair; bit-exact. */
+q_error_code qh_rope_f32(const float* x, const float* cos, const float* sin, float* output,
+                         uint32_t N, uint32_t n_vec, qh_stream s);
+/* Reference src/ops/avx2/silu.c:18-94; bit-exact on the first N&~7 elements. */
+q_error_code qh_silu_f32(const float* x, float* output, uint32_t N, qh_stream s);
+/* silu(gate) * up, the SwiGLU product of reference model.c:1516-1549. */
+q_error_code qh_silu_mul_f32(const float* gate, const float* up, float* output, uint32_t N,
+                             qh_stream s);
+/* Reference src/ops/avx2/softmax.c:17-132 (sum reduced as a fixed tree);
+ * x may alias output. */
+q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream s);
+q_error_code qh_add_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s);
+q_error_code qh_mul_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s);
+/* Greedy argmax of reference src/main.c:870-881 (first index of the
+ * maximum); writes the index to device memory *index_out. */
+q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QORUS_HIP_H */

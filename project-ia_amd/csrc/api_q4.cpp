@@ -1,0 +1,186 @@
+// api_q4.cpp -- Q4_0 dequantization and GEMV entry points.
+//
+// Host-pointer entry points (qorus.h) keep the reference's signature,
+// validation order and return codes; device entry points (qorus_hip.h) share
+// the same validation and enqueue on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+
+#include "qh_kernels.hpp"
+#include "qh_runtime.hpp"
+
+namespace qh {
+
+// Validation of reference src/ops/avx2/matmul.c:104-197, in its order:
+// NULL W/x/y -> INVALID_ARG; x or y not 32-byte aligned -> MISALIGNED;
+// x == y -> ALIASING; M == 0, N == 0, N % 32 -> INVALID_SIZE; type !=
+// Q4_0 -> INVALID_DTYPE; N/32 > UINT32_MAX/M -> OVERFLOW; nb[0] != N/32*20
+// -> INVALID_ARG.  Then, for the device kernel: W->data NULL -> INVALID_ARG
+// and W->data not 4-byte aligned -> MISALIGNED (the reference reads any
+// address; the GPU loads are dword-granular).
+q_error_code validate_gemv(const q_tensor* W, const float* x, const float* y) {
+    if (!W || !x || !y) return Q_ERR_INVALID_ARG;
+    if (!aligned(x, 32) || !aligned(y, 32)) return Q_ERR_MISALIGNED;
+    if (x == y) return Q_ERR_ALIASING;
+    const uint32_t M = W->ne[0], N = W->ne[1];
+    if (M == 0 || N == 0 || N % 32 != 0) return Q_ERR_INVALID_SIZE;
+    if (W->type != Q_Q4_0) return Q_ERR_INVALID_DTYPE;
+    const uint32_t bpr = N / 32;
+    if (bpr > UINT32_MAX / M) return Q_ERR_OVERFLOW;
+    if (W->nb[0] != (size_t)bpr * sizeof(q_block_q4_0)) return Q_ERR_INVALID_ARG;
+    if (!W->data) return Q_ERR_INVALID_ARG;
+    if (!aligned(W->data, 4)) return Q_ERR_MISALIGNED;
+    return Q_OK;
+}
+
+// Library-owned GEMV workspace for device calls that pass none.
+static std::mutex g_ws_mu;
+static void* g_ws = nullptr;
+static size_t g_ws_bytes = 0;
+
+static q_error_code default_workspace(size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (g_ws_bytes < bytes) {
+        if (g_ws) {
+            QH_TRY(hipDeviceSynchronize());
+            QH_TRY(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+        }
+        QH_TRY(hipMalloc(&g_ws, bytes));
+        g_ws_bytes = bytes;
+    }
+    *out = g_ws;
+    return Q_OK;
+}
+
+static q_error_code gemv_device(const q_tensor* W, const void* wdev, const float* x, const float* res,
+                                float* y, void* ws, hipStream_t s) {
+    const uint32_t M = W->ne[0], N = W->ne[1];
+    uint4* xd = static_cast<uint4*>(ws);
+    QH_TRY(launch_xprep(x, N, nullptr, 0.0f, nullptr, xd, s));
+    GemvSeg seg{static_cast<const uint8_t*>(wdev), y, res, M};
+    QH_TRY(launch_gemv(&seg, 1, N / 32, xd, s));
+    return Q_OK;
+}
+
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+size_t qh_gemv_workspace_bytes(uint32_t N) { return xd_bytes((N + 31) / 32); }
+
+q_error_code qh_dequantize_q4_0(const void* blocks, float* out, uint64_t n_blocks, qh_stream s) {
+    if (!blocks || !out) return Q_ERR_INVALID_ARG;
+    if (!aligned(blocks, 4) || !aligned(out, 16)) return Q_ERR_MISALIGNED;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_dequant(static_cast<const uint8_t*>(blocks), out, n_blocks, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_gemv_q4_f32(const q_tensor* W, const float* x, float* y, void* workspace, qh_stream s) {
+    QH_TRY_CODE(validate_gemv(W, x, y));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    if (!workspace) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    return gemv_device(W, W->data, x, nullptr, y, workspace, (hipStream_t)s);
+}
+
+q_error_code qh_gemv_q4_f32_add(const q_tensor* W, const float* x, const float* residual, float* y,
+                                void* workspace, qh_stream s) {
+    QH_TRY_CODE(validate_gemv(W, x, y));
+    if (!residual) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    if (!workspace) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    return gemv_device(W, W->data, x, residual, y, workspace, (hipStream_t)s);
+}
+
+q_error_code qh_gemv_prepare(const float* x, uint32_t N, void* workspace, qh_stream s) {
+    if (!x || !workspace) return Q_ERR_INVALID_ARG;
+    if (!aligned(x, 32)) return Q_ERR_MISALIGNED;
+    if (N == 0 || N % 32 != 0) return Q_ERR_INVALID_SIZE;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_xprep(x, N, nullptr, 0.0f, nullptr, static_cast<uint4*>(workspace), (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* const* residuals,
+                                     float* const* ys, uint32_t n, const void* workspace, qh_stream s) {
+    if (!Ws || !ys || !workspace) return Q_ERR_INVALID_ARG;
+    if (n < 1 || n > 4) return Q_ERR_INVALID_SIZE;
+    GemvSeg segs[4];
+    for (uint32_t i = 0; i < n; ++i) {
+        const q_tensor* W = Ws[i];
+        if (!W || !ys[i]) return Q_ERR_INVALID_ARG;
+        if (!aligned(ys[i], 32)) return Q_ERR_MISALIGNED;
+        const uint32_t M = W->ne[0], N = W->ne[1];
+        if (M == 0 || N == 0 || N % 32 != 0 || N != Ws[0]->ne[1]) return Q_ERR_INVALID_SIZE;
+        if (W->type != Q_Q4_0) return Q_ERR_INVALID_DTYPE;
+        if (N / 32 > UINT32_MAX / M) return Q_ERR_OVERFLOW;
+        if (W->nb[0] != (size_t)(N / 32) * sizeof(q_block_q4_0)) return Q_ERR_INVALID_ARG;
+        if (!W->data) return Q_ERR_INVALID_ARG;
+        if (!aligned(W->data, 4)) return Q_ERR_MISALIGNED;
+        segs[i] = GemvSeg{static_cast<const uint8_t*>(W->data), ys[i], residuals ? residuals[i] : nullptr, M};
+    }
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_gemv(segs, (int)n, Ws[0]->ne[1] / 32, static_cast<const uint4*>(workspace), (hipStream_t)s));
+    return Q_OK;
+}
+
+// Reference src/ops/avx2/dequantize.c:82-96: silent return on NULL.
+void q_dequantize_q4_0_block_avx2_public(const q_block_q4_0* __restrict__ block, float* __restrict__ output) {
+    if (!block || !output) return;
+    Device* d;
+    if (device(&d) != Q_OK) return;
+    std::lock_guard<std::mutex> lk(d->mu);
+    void* buf;
+    if (stage(d, 0, 256, &buf) != Q_OK) return;
+    uint8_t* dblk = static_cast<uint8_t*>(buf);
+    float* dout = reinterpret_cast<float*>(dblk + 64);
+    if (hipMemcpyAsync(dblk, block, 20, hipMemcpyHostToDevice, d->stream) != hipSuccess) return;
+    if (launch_dequant(dblk, dout, 1, d->stream) != hipSuccess) return;
+    if (hipMemcpyAsync(output, dout, 128, hipMemcpyDeviceToHost, d->stream) != hipSuccess) return;
+    (void)hipStreamSynchronize(d->stream);
+}
+
+// Reference src/ops/avx2/matmul.c:98-271 (host pointers, synchronous).
+q_error_code q_gemv_q4_f32_avx2(const q_tensor* __restrict__ weights, const float* __restrict__ input,
+                                float* __restrict__ output) {
+    QH_TRY_CODE(validate_gemv(weights, input, output));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    const uint32_t M = weights->ne[0], N = weights->ne[1];
+    const size_t wbytes = (size_t)M * weights->nb[0];
+    const void* wdev = resident_alias(weights->data, wbytes);
+    hipStream_t s = d->stream;
+    if (!wdev) {
+        void* wbuf;
+        QH_TRY_CODE(stage(d, 0, wbytes, &wbuf));
+        QH_TRY(hipMemcpyAsync(wbuf, weights->data, wbytes, hipMemcpyHostToDevice, s));
+        wdev = wbuf;
+    }
+    const size_t xb = ((size_t)N * 4 + 255) & ~(size_t)255;
+    void* vbuf;
+    QH_TRY_CODE(stage(d, 1, xb + (size_t)M * 4, &vbuf));
+    float* dx = static_cast<float*>(vbuf);
+    float* dy = reinterpret_cast<float*>(static_cast<uint8_t*>(vbuf) + xb);
+    void* ws;
+    QH_TRY_CODE(stage(d, 2, qh_gemv_workspace_bytes(N), &ws));
+    QH_TRY(hipMemcpyAsync(dx, input, (size_t)N * 4, hipMemcpyHostToDevice, s));
+    QH_TRY_CODE(gemv_device(weights, wdev, dx, nullptr, dy, ws, s));
+    QH_TRY(hipMemcpyAsync(output, dy, (size_t)M * 4, hipMemcpyDeviceToHost, s));
+    QH_TRY(hipStreamSynchronize(s));
+    return Q_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,260 @@
+// api_vec.cpp -- RMSNorm, RoPE, SiLU, softmax, add, mul and argmax entry
+// points.  Host-pointer functions (qorus.h) reproduce the reference's
+// validation order and codes, stage their arrays through HBM and return
+// after the result is back on the host; qh_* functions (qorus_hip.h) take
+// device pointers and enqueue on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+
+#include "qh_kernels.hpp"
+#include "qh_runtime.hpp"
+
+namespace qh {
+
+// Carves one staging slot into 256-byte aligned device arrays.
+struct Stager {
+    Device* d = nullptr;
+    uint8_t* base = nullptr;
+    size_t off = 0;
+    static size_t round(size_t b) { return (b + 255) & ~(size_t)255; }
+    q_error_code open(Device* dev, size_t total) {
+        d = dev;
+        void* p;
+        QH_TRY_CODE(stage(dev, 1, total, &p));
+        base = static_cast<uint8_t*>(p);
+        off = 0;
+        return Q_OK;
+    }
+    float* take(size_t n_floats) {
+        float* p = reinterpret_cast<float*>(base + off);
+        off += round(n_floats * 4);
+        return p;
+    }
+    q_error_code put(float* dst, const float* src, size_t n) {
+        if (n) QH_TRY(hipMemcpyAsync(dst, src, n * 4, hipMemcpyHostToDevice, d->stream));
+        return Q_OK;
+    }
+    q_error_code get(float* dst, const float* src, size_t n) {
+        if (n) QH_TRY(hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToHost, d->stream));
+        QH_TRY(hipStreamSynchronize(d->stream));
+        return Q_OK;
+    }
+};
+
+static q_error_code validate_rmsnorm(const float* x, const float* w, const float* y, uint32_t N) {
+    // reference src/ops/avx2/rmsnorm.c:22-31
+    if (!x || !w || !y) return Q_ERR_INVALID_ARG;
+    if (!aligned(x, 32) || !aligned(w, 32) || !aligned(y, 32)) return Q_ERR_MISALIGNED;
+    if (N == 0 || N % 8 != 0) return Q_ERR_INVALID_SIZE;
+    return Q_OK;
+}
+
+static q_error_code validate_rope(const float* x, const float* c, const float* s, const float* y, uint32_t N) {
+    // reference src/ops/avx2/rope.c:32-43
+    if (!x || !c || !s || !y) return Q_ERR_INVALID_ARG;
+    if (!aligned(x, 32) || !aligned(c, 32) || !aligned(s, 32) || !aligned(y, 32)) return Q_ERR_MISALIGNED;
+    if (N == 0 || N % 8 != 0 || N % 2 != 0) return Q_ERR_INVALID_SIZE;
+    return Q_OK;
+}
+
+static q_error_code validate_silu(const float* x, const float* y, uint32_t N) {
+    // reference src/ops/avx2/silu.c:24-64 (alignment only checked for N >= 8)
+    if (!x || !y) return Q_ERR_INVALID_ARG;
+    if (N == 0) return Q_ERR_INVALID_SIZE;
+    if (N >= 8 && (!aligned(x, 32) || !aligned(y, 32))) return Q_ERR_MISALIGNED;
+    return Q_OK;
+}
+
+static q_error_code validate_softmax(const float* x, const float* y, uint32_t N) {
+    // reference src/ops/avx2/softmax.c:23-155 (alignment only checked for N >= 8)
+    if (!x || !y) return Q_ERR_INVALID_ARG;
+    if (N == 0) return Q_ERR_INVALID_SIZE;
+    if (N >= 8 && (!aligned(x, 32) || !aligned(y, 32))) return Q_ERR_MISALIGNED;
+    return Q_OK;
+}
+
+// reference src/ops/avx2/add_fp32.c:23-115 (mul_fp32.c:23-77 is identical).
+static q_error_code validate_binary(const q_tensor* a, const q_tensor* b, const q_tensor* o, uint32_t* N) {
+    if (!a || !b || !o) return Q_ERR_INVALID_ARG;
+    if (!a->data || !b->data || !o->data) return Q_ERR_INVALID_ARG;
+    if (!(a->ne[1] == 1 && a->ne[2] == 1 && a->ne[3] == 1)) return Q_ERR_INVALID_SIZE;
+    if (!(b->ne[1] == 1 && b->ne[2] == 1 && b->ne[3] == 1)) return Q_ERR_INVALID_SIZE;
+    if (!(o->ne[1] == 1 && o->ne[2] == 1 && o->ne[3] == 1)) return Q_ERR_INVALID_SIZE;
+    const uint32_t n = a->ne[0];
+    if (n != b->ne[0] || n != o->ne[0]) return Q_ERR_INVALID_SIZE;
+    if (a->type != Q_F32 || b->type != Q_F32 || o->type != Q_F32) return Q_ERR_INVALID_DTYPE;
+    const size_t row = (size_t)n * sizeof(float);
+    if (a->nb[0] != row || b->nb[0] != row || o->nb[0] != row) return Q_ERR_INVALID_SIZE;
+    if (!aligned(a->data, 32) || !aligned(b->data, 32) || !aligned(o->data, 32)) return Q_ERR_MISALIGNED;
+    *N = n;
+    return Q_OK;
+}
+
+static q_error_code host_binary(const q_tensor* a, const q_tensor* b, q_tensor* o, int op) {
+    uint32_t N = 0;
+    QH_TRY_CODE(validate_binary(a, b, o, &N));
+    if (N == 0) return Q_OK;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, 3 * Stager::round((size_t)N * 4)));
+    float* da = st.take(N);
+    float* db = st.take(N);
+    float* dout = st.take(N);
+    QH_TRY_CODE(st.put(da, static_cast<const float*>(a->data), N));
+    QH_TRY_CODE(st.put(db, static_cast<const float*>(b->data), N));
+    QH_TRY(launch_binary(da, db, dout, N, op, d->stream));
+    return st.get(static_cast<float*>(o->data), dout, N);
+}
+
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+q_error_code q_rmsnorm_f32_avx2(const float* __restrict__ x, const float* __restrict__ weight,
+                                float* __restrict__ output, uint32_t N, float eps) {
+    QH_TRY_CODE(validate_rmsnorm(x, weight, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, 3 * Stager::round((size_t)N * 4)));
+    float* dx = st.take(N);
+    float* dw = st.take(N);
+    float* dy = st.take(N);
+    QH_TRY_CODE(st.put(dx, x, N));
+    QH_TRY_CODE(st.put(dw, weight, N));
+    QH_TRY(launch_rmsnorm(dx, dw, dy, N, eps, d->stream));
+    return st.get(output, dy, N);
+}
+
+q_error_code q_rope_f32_avx2(const float* __restrict__ x, const float* __restrict__ cos,
+                             const float* __restrict__ sin, float* __restrict__ output, uint32_t N) {
+    QH_TRY_CODE(validate_rope(x, cos, sin, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, 4 * Stager::round((size_t)N * 4)));
+    float* dx = st.take(N);
+    float* dc = st.take(N);
+    float* ds = st.take(N);
+    float* dy = st.take(N);
+    QH_TRY_CODE(st.put(dx, x, N));
+    QH_TRY_CODE(st.put(dc, cos, N));
+    QH_TRY_CODE(st.put(ds, sin, N));
+    QH_TRY(launch_rope(dx, dc, ds, dy, N, 1, d->stream));
+    return st.get(output, dy, N);
+}
+
+q_error_code q_silu_f32_avx2(const float* __restrict__ x, float* __restrict__ output, uint32_t N) {
+    QH_TRY_CODE(validate_silu(x, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, 2 * Stager::round((size_t)N * 4)));
+    float* dx = st.take(N);
+    float* dy = st.take(N);
+    QH_TRY_CODE(st.put(dx, x, N));
+    QH_TRY(launch_silu(dx, nullptr, dy, N, d->stream));
+    return st.get(output, dy, N);
+}
+
+q_error_code q_softmax_f32_avx2(const float* __restrict__ x, float* __restrict__ output, uint32_t N) {
+    QH_TRY_CODE(validate_softmax(x, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, Stager::round((size_t)N * 4)));
+    float* dx = st.take(N);
+    QH_TRY_CODE(st.put(dx, x, N));
+    QH_TRY(launch_softmax(dx, dx, N, d->stream));
+    return st.get(output, dx, N);
+}
+
+q_error_code q_add_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output) {
+    return host_binary(a, b, output, 0);
+}
+
+q_error_code q_mul_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output) {
+    return host_binary(a, b, output, 1);
+}
+
+// ---- device entry points ----
+
+q_error_code qh_rmsnorm_f32(const float* x, const float* weight, float* output, uint32_t N, float eps,
+                            qh_stream s) {
+    QH_TRY_CODE(validate_rmsnorm(x, weight, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_rmsnorm(x, weight, output, N, eps, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_rope_f32(const float* x, const float* cos, const float* sin, float* output, uint32_t N,
+                         uint32_t n_vec, qh_stream s) {
+    QH_TRY_CODE(validate_rope(x, cos, sin, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_rope(x, cos, sin, output, N, n_vec, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_silu_f32(const float* x, float* output, uint32_t N, qh_stream s) {
+    QH_TRY_CODE(validate_silu(x, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_silu(x, nullptr, output, N, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_silu_mul_f32(const float* gate, const float* up, float* output, uint32_t N, qh_stream s) {
+    QH_TRY_CODE(validate_silu(gate, output, N));
+    if (!up) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_silu(gate, up, output, N, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream s) {
+    QH_TRY_CODE(validate_softmax(x, output, N));
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_softmax(x, output, N, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_add_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s) {
+    if (!a || !b || !output) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_binary(a, b, output, N, 0, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_mul_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s) {
+    if (!a || !b || !output) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_binary(a, b, output, N, 1, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_stream s) {
+    if (!x || !index_out) return Q_ERR_INVALID_ARG;
+    if (N == 0) return Q_ERR_INVALID_SIZE;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_argmax(x, N, index_out, (hipStream_t)s));
+    return Q_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,206 @@
+// k_vec.hip -- vector kernels of the decode step for gfx950: RMSNorm, RoPE,
+// SiLU (and the fused SwiGLU product), softmax, add, mul, argmax.
+//
+// Bit-exactness with the reference: RoPE, add, mul, the polynomial exp, the
+// vector part of SiLU and every per-element softmax step are the same IEEE
+// operations in the same order, so they are bit-exact.  Reductions (the
+// RMSNorm sum of squares, the softmax sum) use a fixed tree instead of the
+// reference's 8 sequential lane chains, so their last bit can differ; the
+// reference's RMSNorm bits are CPU-specific anyway (rsqrtps seed).  The
+// N%8 tails of SiLU/softmax call the device expf where the reference calls
+// glibc expf (parity at that libm boundary is tolerance-only).
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "qh_kernels.hpp"
+#include "qh_vec.hpp"
+
+namespace qh {
+
+constexpr int kVecThreads = 1024;
+
+// RMSNorm, one workgroup: y = (x*r)*w (reference src/ops/avx2/rmsnorm.c:166-176).
+__global__ __launch_bounds__(kVecThreads) void k_rmsnorm(const float* __restrict__ x,
+                                                         const float* __restrict__ w, float* __restrict__ y,
+                                                         uint32_t N, float eps) {
+    __shared__ float red[kVecThreads / 64];
+    const float r = rms_scale<kVecThreads>(x, N, eps, red);
+    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) {
+        const float n = x[i] * r;
+        y[i] = n * w[i];
+    }
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kVecThreads), 0, s, x, w, y, N, eps);
+    return hipGetLastError();
+}
+
+// RoPE over n_vec vectors of length N sharing one table pair
+// (reference src/ops/avx2/rope.c:244-285): y0 = x0*c - x1*s, y1 = x1*c + x0*s.
+__global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, const float* __restrict__ ct,
+                                              const float* __restrict__ st, float* __restrict__ y,
+                                              uint32_t N, uint32_t total_pairs) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= total_pairs) return;
+    const uint32_t half = N / 2;
+    const uint32_t v = p / half, i = 2 * (p % half);
+    const float2 xv = *reinterpret_cast<const float2*>(x + (size_t)v * N + i);
+    const float c = ct[i], sn = st[i];
+    const float a0 = xv.x * c, b0 = xv.y * sn;
+    const float a1 = xv.y * c, b1 = xv.x * sn;
+    *reinterpret_cast<float2*>(y + (size_t)v * N + i) = make_float2(a0 - b0, a1 + b1);
+}
+
+hipError_t launch_rope(const float* x, const float* ct, const float* st, float* y, uint32_t N, uint32_t n_vec,
+                       hipStream_t s) {
+    const uint32_t total = (N / 2) * n_vec;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope, dim3((total + 255) / 256), dim3(256), 0, s, x, ct, st, y, N, total);
+    return hipGetLastError();
+}
+
+// SiLU (reference src/ops/avx2/silu.c:44-91).  With u != nullptr the output
+// is silu(x)*u, the SwiGLU product of reference src/models/model.c:1516-1549.
+__global__ __launch_bounds__(256) void k_silu(const float* __restrict__ x, const float* __restrict__ u,
+                                              float* __restrict__ y, uint32_t N) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t nv = (N >= 8) ? (N & ~7u) : 0u;
+    const float xv = x[i];
+    float r;
+    if (i < nv) {
+        r = silu_approx(xv);
+    } else {
+        const float sg = 1.0f / (1.0f + expf(-xv));
+        r = xv * sg;
+    }
+    y[i] = u ? r * u[i] : r;
+}
+
+hipError_t launch_silu(const float* x, const float* u, float* y, uint32_t N, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu, dim3((N + 255) / 256), dim3(256), 0, s, x, u, y, N);
+    return hipGetLastError();
+}
+
+// Softmax, one workgroup (reference src/ops/avx2/softmax.c:30-213).
+// N >= 8: m = max; e_i = exp_approx(x_i - m) for i < N&~7 (tree sum), tail
+// e_i = expf(x_i - m) added in index order after the vector sum, inv =
+// 1/sum, y_i = e_i*inv.  N < 8: expf, sequential sum, y_i = e_i/sum.
+// x may alias y.
+__global__ __launch_bounds__(kVecThreads) void k_softmax(const float* x, float* y, uint32_t N) {
+    __shared__ float red[kVecThreads / 64];
+    if (N < 8) {
+        if (threadIdx.x == 0) {
+            float mx = x[0];
+            for (uint32_t i = 1; i < N; ++i)
+                if (x[i] > mx) mx = x[i];
+            float e[8];
+            float sum = 0.0f;
+            for (uint32_t i = 0; i < N; ++i) {
+                e[i] = expf(x[i] - mx);
+                sum += e[i];
+            }
+            for (uint32_t i = 0; i < N; ++i) y[i] = e[i] / sum;
+        }
+        return;
+    }
+    const uint32_t nv = N & ~7u;
+    float m = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) m = fmaxf(m, x[i]);
+    m = block_max<kVecThreads>(m, red);
+    float ls = 0.0f;
+    for (uint32_t i = threadIdx.x; i < nv; i += kVecThreads) {
+        const float d = x[i] - m;
+        const float e = exp_approx(d);
+        ls = ls + e;
+        y[i] = e;
+    }
+    if (threadIdx.x == 0) {
+        for (uint32_t i = nv; i < N; ++i) y[i] = expf(x[i] - m);
+    }
+    float sum = block_sum<kVecThreads>(ls, red);  // its barriers publish the tail values
+    // Sequential tail additions after the vector sum, in index order.
+    for (uint32_t i = nv; i < N; ++i) sum = sum + y[i];
+    __syncthreads();  // every thread has read the tails before any is rescaled
+    const float inv = 1.0f / sum;
+    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) y[i] = y[i] * inv;
+}
+
+hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_softmax, dim3(1), dim3(kVecThreads), 0, s, x, y, N);
+    return hipGetLastError();
+}
+
+// Elementwise add / mul (reference add_fp32.c:127-161, mul_fp32.c:89-123).
+__global__ __launch_bounds__(256) void k_binary(const float* a, const float* b, float* o, uint32_t N, int op) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const float av = a[i], bv = b[i];
+    o[i] = op == 0 ? av + bv : av * bv;
+}
+
+hipError_t launch_binary(const float* a, const float* b, float* o, uint32_t N, int op, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_binary, dim3((N + 255) / 256), dim3(256), 0, s, a, b, o, N, op);
+    return hipGetLastError();
+}
+
+// Greedy argmax (reference src/main.c:870-881): first index of the maximum
+// under strict '>' scanning from index 0; NaN entries never win; a NaN at
+// index 0 makes the answer 0.
+__device__ __forceinline__ bool arg_better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(kVecThreads) void k_argmax(const float* __restrict__ x, uint32_t N,
+                                                        uint32_t* __restrict__ out) {
+    __shared__ float sv[kVecThreads / 64];
+    __shared__ uint32_t si[kVecThreads / 64];
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) {
+        const float v = x[i];
+        if (arg_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (arg_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = sv[0];
+        uint32_t i = si[0];
+        for (int k = 1; k < kVecThreads / 64; ++k)
+            if (arg_better(sv[k], si[k], v, i)) {
+                v = sv[k];
+                i = si[k];
+            }
+        if (N > 0 && x[0] != x[0]) i = 0;  // NaN at index 0: nothing compares greater
+        if (i == 0xFFFFFFFFu) i = 0;
+        *out = i;
+    }
+}
+
+hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, out);
+    return hipGetLastError();
+}
+
+}  // namespace qh

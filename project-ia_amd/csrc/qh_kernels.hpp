@@ -1,0 +1,55 @@
+// qh_kernels.hpp -- host-side launchers of the gfx950 kernels.  Launchers
+// assume validated arguments (the C-ABI layer checks them) and return the
+// hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace qh {
+
+// ---- Q4_0 ----
+
+// Dequantize n_blocks 20-byte blocks into 32*n_blocks floats (bit-exact).
+hipError_t launch_dequant(const uint8_t* blocks, float* out, uint64_t n_blocks, hipStream_t s);
+
+// x-digit planes ("xd"): per 32-element block of x, the signed 4-bit digits
+// of round(x * 2^k) in 6 planes (uint4 each), plus (k, NaN-injection word).
+// Layout: uint4 xd[7][nblk_pad]; plane t of block c at xd[t * nblk_pad + c].
+constexpr int kXdPlanes = 7;
+inline uint32_t xd_pad(uint32_t nblk) { return (nblk + 63u) & ~63u; }
+inline size_t xd_bytes(uint32_t nblk) { return (size_t)kXdPlanes * xd_pad(nblk) * 16u; }
+
+// Fused RMSNorm (optional) + digit-plane preparation of an input vector.
+// With norm_w != nullptr: h = rmsnorm(x, norm_w, eps) (reference order) is
+// written to h_out (if non-null) and its digits to xd; else x's digits.
+hipError_t launch_xprep(const float* x, uint32_t N, const float* norm_w, float eps, float* h_out,
+                        uint4* xd, hipStream_t s);
+
+// One GEMV "segment": rows [0, M) of a Q4_0 matrix with N = 32*nblk columns.
+struct GemvSeg {
+    const uint8_t* w;     // device AoS blocks
+    float* y;             // output [M]
+    const float* res;     // optional residual [M] (y = res + W.x)
+    uint32_t M;
+};
+
+// y = W . x for up to 4 segments sharing the same x (digit planes xd).
+hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd,
+                       hipStream_t s);
+
+// ---- vector kernels (k_vec.hip) ----
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s);
+// RoPE of n_vec consecutive vectors of length N with one cos/sin table pair.
+hipError_t launch_rope(const float* x, const float* ct, const float* st, float* y, uint32_t N,
+                       uint32_t n_vec, hipStream_t s);
+// y = silu(x) (u == nullptr) or silu(x) * u.
+hipError_t launch_silu(const float* x, const float* u, float* y, uint32_t N, hipStream_t s);
+hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s);
+// op 0: o = a + b; op 1: o = a * b.
+hipError_t launch_binary(const float* a, const float* b, float* o, uint32_t N, int op, hipStream_t s);
+hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t s);
+
+}  // namespace qh

@@ -1,0 +1,70 @@
+// qh_runtime.hpp -- internal runtime of libqorus_hip.so: HIP error mapping,
+// per-process device state (library stream, grow-only staging buffers) and
+// the side table that attaches HBM state to a q_context without changing
+// the q_context layout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "qorus.h"
+#include "qorus_hip.h"
+
+namespace qh {
+
+// Records the HIP error text for qh_last_error() and maps it to a q_error_code.
+q_error_code fail(hipError_t e, const char* what);
+
+#define QH_TRY(expr)                                        \
+    do {                                                    \
+        hipError_t qh_e_ = (expr);                          \
+        if (qh_e_ != hipSuccess) return ::qh::fail(qh_e_, #expr); \
+    } while (0)
+
+#define QH_TRY_CODE(expr)                   \
+    do {                                    \
+        q_error_code qh_c_ = (expr);        \
+        if (qh_c_ != Q_OK) return qh_c_;    \
+    } while (0)
+
+// Process-wide device state, created on first use.  Every HIP resource the
+// library owns (stream, staging buffers) lives here; the op entry points of
+// qorus.h run on `stream` and synchronize before returning.
+struct Device {
+    int id = -1;
+    hipStream_t stream = nullptr;
+    std::mutex mu;  // serializes the synchronous host-pointer entry points
+    // Grow-only device staging used by the host-pointer entry points.
+    void* stage[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t stage_bytes[4] = {0, 0, 0, 0};
+};
+
+// Returns Q_OK and the initialized device, or an error if no GPU is usable.
+q_error_code device(Device** out);
+
+// Ensures staging slot `slot` holds at least `bytes`; returns its address.
+q_error_code stage(Device* d, int slot, size_t bytes, void** out);
+
+// HBM mirror of a q_context (side table keyed by the context address).
+struct CtxState {
+    q_context* ctx = nullptr;
+    uint8_t* dev_weights = nullptr;  // HBM copy of the mapped .qorus file
+    size_t weights_size = 0;
+    uint8_t* dev_arena = nullptr;    // decode-step scratch (allocated by llama_build_graph)
+    size_t dev_arena_size = 0;
+    void* plan = nullptr;            // ModelPlan* (model.cpp)
+};
+
+CtxState* ctx_state(const q_context* ctx, bool create);
+void ctx_state_erase(const q_context* ctx);
+
+// If [p, p+bytes) lies inside the host mapping of a registered context whose
+// weights are HBM-resident, returns the device address of p; else nullptr.
+const void* resident_alias(const void* p, size_t bytes);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace qh

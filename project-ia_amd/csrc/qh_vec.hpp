@@ -1,0 +1,91 @@
+// qh_vec.hpp -- device helpers shared by the vector kernels: the reference's
+// polynomial exp and the workgroup reductions.  Header-only, HIP device code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qh {
+
+// Polynomial exp of reference src/ops/avx2/avx_math.h:10-61, bit-exact:
+// flags on the unclamped x (ordered compares), clamp with x86 minps/maxps
+// semantics ((a<b)?a:b, (a>b)?a:b), degree-5 Horner in fmaf, max(r,0),
+// x < -10 -> 0, x > 10 -> 22026.
+__device__ __forceinline__ float exp_approx(float x) {
+    const bool very_neg = x < -10.0f;
+    const bool very_pos = x > 10.0f;
+    float t = (x < 5.0f) ? x : 5.0f;
+    t = (t > -5.0f) ? t : -5.0f;
+    float r = 0.00833333f;
+    r = fmaf(r, t, 0.04166667f);
+    r = fmaf(r, t, 0.16666667f);
+    r = fmaf(r, t, 0.5f);
+    r = fmaf(r, t, 1.0f);
+    r = fmaf(r, t, 1.0f);
+    r = (r > 0.0f) ? r : 0.0f;
+    if (very_neg) r = 0.0f;
+    if (very_pos) r = 22026.0f;
+    return r;
+}
+
+// SiLU of reference src/ops/avx2/silu.c:75-82 (vector part).
+__device__ __forceinline__ float silu_approx(float x) {
+    const float e = exp_approx(-x);
+    const float d = 1.0f + e;
+    const float sg = 1.0f / d;
+    return x * sg;
+}
+
+// Fixed-order workgroup sum for blockDim.x == NT (multiple of 64): wave
+// butterflies, then the wave partials in index order.  Every thread gets the
+// result.  `red` needs NT/64 floats of shared memory.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) s += red[i];
+    __syncthreads();
+    return s;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) s = fmaxf(s, red[i]);
+    __syncthreads();
+    return s;
+}
+
+// RMSNorm scale r for x[0..N) (fixed-order tree sum of squares; mean =
+// sum/(float)N; a = mean + eps; r0 = rsq(a); one Newton step
+// (r0*(3 - a*(r0*r0)))*0.5 as in reference src/ops/avx2/rmsnorm.c:62-71).
+template <int NT>
+__device__ __forceinline__ float rms_scale(const float* __restrict__ x, uint32_t N, float eps, float* red) {
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < N; i += NT) {
+        const float v = x[i];
+        const float sq = v * v;
+        ss = ss + sq;
+    }
+    const float sum = block_sum<NT>(ss, red);
+    const float mean = sum / (float)N;
+    const float a = mean + eps;
+    const float r0 = __builtin_amdgcn_rsqf(a);
+    const float rr = r0 * r0;
+    const float ar = a * rr;
+    const float t = 3.0f - ar;
+    const float r1 = r0 * t;
+    return r1 * 0.5f;
+}
+
+}  // namespace qh

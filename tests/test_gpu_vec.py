@@ -1,0 +1,132 @@
+"""GPU parity of the vector ops that feed the GEMV in the decode step,
+through the C-ABI (host-pointer qorus.h entry points and device qh_* ones).
+
+Bars, written out:
+  RoPE, add, mul, SiLU on its first N&~7 elements: bit-exact with the oracle
+    (the same IEEE operations in the same order);
+  SiLU/softmax N%8 tails (libm expf there, device expf here): <= 2 ulp;
+  RMSNorm: relative error <= 2e-6 (reduction order + reciprocal-sqrt seed);
+  softmax: relative error <= 2e-6, and exactly the same zero pattern
+    (the polynomial's zeroing is bit-exact; only the sum order differs);
+  argmax: identical index, first index on ties.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def ulp_diff(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def host(n):
+    return orc.aligned_empty((n,), np.float32)
+
+
+@pytest.mark.parametrize("N", [8, 128, 4096, 14336])
+def test_rmsnorm(qa, N):
+    rng = orc.rng_for(201, N)
+    x, w = orc.aligned_copy(orc.gen_f32(N, rng)), orc.aligned_copy(orc.gen_f32(N, rng))
+    y = host(N)
+    assert qa.lib().q_rmsnorm_f32_avx2(x.ctypes.data, w.ctypes.data, y.ctypes.data, N, 1e-5) == 0
+    want = orc.rmsnorm(x, w, 1e-5)
+    assert np.max(np.abs(y - want) / (np.abs(want) + 1e-30)) <= 2e-6
+    # device entry point gives the same bits as the host one
+    dx, dw, dy = (qa.DeviceBuffer.from_numpy(a) for a in (x, w, y))
+    qa.check(qa.lib().qh_rmsnorm_f32(dx.ptr, dw.ptr, dy.ptr, N, 1e-5, None))
+    qa.check(qa.lib().qh_device_synchronize())
+    assert np.array_equal(bits(dy.download(np.float32, (N,))), bits(y))
+
+
+def test_rope_bitexact(qa):
+    rng = orc.rng_for(202)
+    for pos in (0, 1, 2047, 8191):
+        c, s = (orc.aligned_copy(t) for t in orc.rope_tables(500000.0, 128, pos))
+        x = orc.aligned_copy(orc.gen_f32(128, rng))
+        y = host(128)
+        assert qa.lib().q_rope_f32_avx2(x.ctypes.data, c.ctypes.data, s.ctypes.data, y.ctypes.data, 128) == 0
+        assert np.array_equal(bits(y), bits(orc.rope(x, c, s)))
+    # batched device form: 40 heads (32 q + 8 k) with one table pair
+    c, s = orc.rope_tables(500000.0, 128, 2047)
+    X = orc.gen_f32(40 * 128, rng)
+    dX, dc, ds, dY = (qa.DeviceBuffer.from_numpy(a) for a in (X, c, s, np.zeros_like(X)))
+    qa.check(qa.lib().qh_rope_f32(dX.ptr, dc.ptr, ds.ptr, dY.ptr, 128, 40, None))
+    qa.check(qa.lib().qh_device_synchronize())
+    Y = dY.download(np.float32, (40 * 128,))
+    want = np.concatenate([orc.rope(X[h * 128:(h + 1) * 128], c, s) for h in range(40)])
+    assert np.array_equal(bits(Y), bits(want))
+
+
+@pytest.mark.parametrize("N", [1, 5, 8, 29, 4096, 14336])
+def test_silu(qa, N):
+    rng = orc.rng_for(203, N)
+    x = orc.aligned_copy((rng.random(N, dtype=np.float32) * 24 - 12).astype(np.float32))
+    y = host(N)
+    assert qa.lib().q_silu_f32_avx2(x.ctypes.data, y.ctypes.data, N) == 0
+    want = orc.silu(x)
+    nv = N & ~7 if N >= 8 else 0
+    assert np.array_equal(bits(y[:nv]), bits(want[:nv]))
+    assert np.all(ulp_diff(y[nv:], want[nv:]) <= 2)
+
+
+def test_silu_mul_fused(qa):
+    rng = orc.rng_for(204)
+    N = 14336
+    g, u = orc.gen_f32(N, rng) * 3, orc.gen_f32(N, rng)
+    dg, du, do = qa.DeviceBuffer.from_numpy(g), qa.DeviceBuffer.from_numpy(u), qa.DeviceBuffer(N * 4)
+    qa.check(qa.lib().qh_silu_mul_f32(dg.ptr, du.ptr, do.ptr, N, None))
+    qa.check(qa.lib().qh_device_synchronize())
+    assert np.array_equal(bits(do.download(np.float32, (N,))), bits(orc.mul(orc.silu(g), u)))
+
+
+@pytest.mark.parametrize("N", [1, 5, 8, 71, 2048, 128256])
+def test_softmax(qa, N):
+    rng = orc.rng_for(205, N)
+    x = orc.aligned_copy(orc.gen_f32(N, rng) * 2)
+    y = host(N)
+    assert qa.lib().q_softmax_f32_avx2(x.ctypes.data, y.ctypes.data, N) == 0
+    want = orc.softmax(x)
+    assert np.array_equal(y == 0, want == 0)
+    nz = want != 0
+    assert np.max(np.abs(y[nz] - want[nz]) / want[nz]) <= 2e-6
+    assert abs(float(y.sum(dtype=np.float64)) - 1.0) < 1e-4
+
+
+def test_add_mul_bitexact(qa):
+    rng = orc.rng_for(206)
+    N = 4096
+    a, b = orc.aligned_copy(orc.gen_f32(N, rng)), orc.aligned_copy(orc.gen_f32(N, rng))
+    o = host(N)
+    ta, tb, to = qa.f32_tensor(a.ctypes.data, N), qa.f32_tensor(b.ctypes.data, N), qa.f32_tensor(o.ctypes.data, N)
+    assert qa.lib().q_add_f32_avx2(ta.addr, tb.addr, to.addr) == 0
+    assert np.array_equal(bits(o), bits(orc.add(a, b)))
+    assert qa.lib().q_mul_f32_avx2(ta.addr, tb.addr, to.addr) == 0
+    assert np.array_equal(bits(o), bits(orc.mul(a, b)))
+    # in place (output aliases a), as the reference allows
+    a0 = a.copy()
+    assert qa.lib().q_add_f32_avx2(ta.addr, tb.addr, ta.addr) == 0
+    assert np.array_equal(bits(a), bits(orc.add(a0, b)))
+
+
+def test_argmax(qa):
+    rng = orc.rng_for(207)
+    cases = [orc.gen_f32(128256, rng), np.array([1, 5, 5, 2, 5], np.float32),
+             np.array([np.nan, 3, 4], np.float32), np.array([2, np.nan, 7, 7], np.float32),
+             np.full(1000, -np.inf, np.float32), np.array([3.0], np.float32)]
+    out = qa.DeviceBuffer(4)
+    for x in cases:
+        dx = qa.DeviceBuffer.from_numpy(x)
+        qa.check(qa.lib().qh_argmax_f32(dx.ptr, x.size, out.ptr, None))
+        qa.check(qa.lib().qh_device_synchronize())
+        assert int(out.download(np.uint32, (1,))[0]) == orc.argmax(x)

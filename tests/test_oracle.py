@@ -1,0 +1,316 @@
+"""Pins the CPU oracle (oracle/qorus_oracle.c) before anything is compared to it.
+
+Each oracle function is checked against (a) the reference's own golden vectors
+(tests/golden, copied from the reference's test_data/), (b) the reference's
+own C compiled from its sources (oracle/_ref, when built), and (c) what the
+mathematics fixes (closed forms in float64, invariants, special cases), so a
+dropped term, swapped index or wrong sign fails at least one check.
+"""
+import math
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+needs_ref = pytest.mark.skipif(not orc.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all((bits(a) == bits(b)) | both_nan))
+
+
+# ---------------------------------------------------------------- dequant --
+
+def load_golden(i):
+    blk = np.frombuffer((GOLDEN / f"dequantize_test{i}_block.bin").read_bytes(), dtype=np.uint8)
+    raw = (GOLDEN / f"dequantize_test{i}_expected.bin").read_bytes()
+    n = struct.unpack_from("<I", raw, 0)[0]
+    exp = np.frombuffer(raw[4:], dtype="<f4")
+    assert n == 32 and exp.size == 32 and blk.size == 20
+    return blk, exp
+
+
+@pytest.mark.parametrize("case", [1, 2, 3, 4])
+def test_dequant_golden(case):
+    blk, exp = load_golden(case)
+    got = orc.dequant(blk)
+    # Values agree exactly; the golden file (numpy (q-8)*s) carries -0 where
+    # the FMA form fmaf(q, s, -8s) gives +0 (reference dequantize.c:54).
+    assert np.array_equal(got, exp)
+    nz = exp != 0
+    assert same_bits(got[nz], exp[nz])
+
+
+def test_dequant_golden_nibble_order():
+    # Golden case 4: byte 0x54 holds elements 4 (low nibble 4) and 5 (high 5).
+    blk, exp = load_golden(4)
+    assert blk[2] == 0x54
+    got = orc.dequant(blk)
+    assert got[4] == -8.0 and got[5] == -6.0
+
+
+def test_dequant_closed_form_random():
+    rng = orc.rng_for(7)
+    W = orc.gen_q4(64, 256, rng)
+    got = orc.dequant(W).reshape(64, 256)
+    want = orc.dequant_np(W).astype(np.float32)  # single rounding of the exact product
+    assert np.array_equal(got, want)
+    assert same_bits(got[want != 0], want[want != 0])
+
+
+ADV_SCALES = [0.0, -1.0, 1e-10, 1e10, 16.0, np.finfo(np.float32).tiny, np.finfo(np.float32).max,
+              float("inf"), float("nan"), -0.0]
+ADV_PATTERNS = [0x88, 0xFF, 0x00, "alt", "rand"]
+
+
+def adv_block(scale, pat, rng):
+    b = np.zeros(20, np.uint8)
+    if pat == "alt":
+        b[:16] = [0x00 if i % 2 == 0 else 0xFF for i in range(16)]
+    elif pat == "rand":
+        b[:16] = rng.integers(0, 256, 16, dtype=np.uint8)
+    else:
+        b[:16] = pat
+    b[16:] = np.frombuffer(np.float32(scale).tobytes(), np.uint8)
+    return b
+
+
+@needs_ref
+@pytest.mark.parametrize("scale", ADV_SCALES)
+@pytest.mark.parametrize("pat", ADV_PATTERNS)
+def test_dequant_matches_reference_build(scale, pat):
+    rng = orc.rng_for(11)
+    b = adv_block(scale, pat, rng)
+    assert same_bits(orc.dequant(b), orc.ref_dequant_block(b))
+
+
+# ------------------------------------------------------------------- GEMV --
+
+GEMV_SHAPES = [(1, 32), (2, 64), (3, 96), (4, 128), (5, 160), (7, 224), (16, 1024), (33, 4096), (8, 14336)]
+
+
+@needs_ref
+@pytest.mark.parametrize("M,N", GEMV_SHAPES)
+def test_gemv_matches_reference_build(M, N):
+    rng = orc.rng_for(21, M, N)
+    W = orc.gen_q4(M, N, rng)
+    x = orc.gen_f32(N, rng)
+    rc, yr = orc.ref_gemv(W, M, N, x)
+    assert rc == 0
+    assert same_bits(orc.gemv(W, M, N, x), yr)
+
+
+@pytest.mark.parametrize("M,N", GEMV_SHAPES)
+def test_gemv_vs_fp64(M, N):
+    rng = orc.rng_for(22, M, N)
+    W = orc.gen_q4(M, N, rng)
+    x = orc.gen_f32(N, rng)
+    y64, cond = orc.gemv_f64(W, M, N, x)
+    # Independent float64 closed form (numpy) agrees with the C fp64 oracle.
+    dq = orc.dequant_np(W)
+    assert np.allclose(dq @ x.astype(np.float64), y64, rtol=1e-12, atol=1e-12)
+    y = orc.gemv(W, M, N, x)
+    assert np.max(np.abs(y - y64) / cond) < 1e-6
+
+
+def test_gemv_single_block_brute_force():
+    # One row, one block: y = sum_e fma-dequant(e) * x_e accumulated per lane l
+    # over k, then the lane tree -- checked against direct enumeration of
+    # which (element, lane) pairs feed which accumulator.
+    rng = orc.rng_for(23)
+    W = orc.gen_q4(1, 32, rng)
+    x = orc.gen_f32(32, rng)
+    w = orc.dequant(W)
+    lane = np.zeros(8, np.float32)
+    for k in range(4):
+        for l in range(8):
+            e = 8 * k + l
+            lane[l] = np.float32(np.float64(w[e]) * np.float64(x[e]) + np.float64(lane[l]))
+    t = [np.float32(lane[j] + lane[j + 4]) for j in range(4)]
+    want = np.float32(np.float32(t[0] + t[1]) + np.float32(t[2] + t[3]))
+    assert orc.gemv(W, 1, 32, x)[0] == want
+
+
+# ------------------------------------------------------------- vector ops --
+
+def test_rmsnorm_closed_form():
+    rng = orc.rng_for(31)
+    for N in (8, 64, 4096):
+        x = orc.gen_f32(N, rng)
+        w = orc.gen_f32(N, rng)
+        y = orc.rmsnorm(x, w, 1e-5)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 * x64) + 1e-5) * w
+        assert np.max(np.abs(y - want) / (np.abs(want) + 1e-30)) < 2e-6
+
+
+@needs_ref
+def test_rmsnorm_vs_reference_build():
+    rng = orc.rng_for(32)
+    for N in (8, 128, 4096):
+        x, w = orc.gen_f32(N, rng), orc.gen_f32(N, rng)
+        rc, yr = orc.ref_rmsnorm(x, w, 1e-5)
+        assert rc == 0
+        # rsqrtps + one Newton step vs 1/sqrtf + one Newton step.
+        assert np.max(np.abs(orc.rmsnorm(x, w, 1e-5) - yr) / (np.abs(yr) + 1e-30)) < 2e-6
+
+
+@needs_ref
+def test_rope_vs_reference_build():
+    rng = orc.rng_for(33)
+    c, s = orc.rope_tables(500000.0, 128, 1234)
+    x = orc.gen_f32(128, rng)
+    rc, yr = orc.ref_rope(x, c, s)
+    assert rc == 0
+    assert same_bits(orc.rope(x, c, s), yr)
+
+
+def test_rope_invariants():
+    rng = orc.rng_for(34)
+    x = orc.gen_f32(128, rng)
+    c0, s0 = orc.rope_tables(500000.0, 128, 0)
+    assert np.array_equal(orc.rope(x, c0, s0), x)  # pos 0 is the identity
+    c, s = orc.rope_tables(500000.0, 128, 777)
+    assert np.array_equal(c[0::2], c[1::2]) and np.array_equal(s[0::2], s[1::2])
+    y = orc.rope(x, c, s).astype(np.float64)
+    x64 = x.astype(np.float64)
+    n_in = x64[0::2] ** 2 + x64[1::2] ** 2
+    n_out = y[0::2] ** 2 + y[1::2] ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5)
+    # Pair 0 rotates by exactly pos radians (freq_0 = base^0 = 1).
+    ang = math.atan2(y[1] * x64[0] - y[0] * x64[1], y[0] * x64[0] + y[1] * x64[1])
+    assert abs(((ang - 777.0) + math.pi) % (2 * math.pi) - math.pi) < 1e-3
+
+
+C3, C4, C5 = (float(np.float32(v)) for v in (0.16666667, 0.04166667, 0.00833333))
+
+
+def exp_poly64(x):
+    """The reference polynomial (its float32 coefficients, reference
+    avx_math.h:36-41) evaluated in float64 as a power sum, with its clamps."""
+    t = min(max(x, -5.0), 5.0)
+    r = 1 + t + 0.5 * t * t + C3 * t ** 3 + C4 * t ** 4 + C5 * t ** 5
+    r = max(r, 0.0)
+    if x < -10:
+        return 0.0
+    if x > 10:
+        return 22026.0
+    return r
+
+
+def test_exp_approx_special_cases():
+    assert orc.exp_approx(0.0) == 1.0
+    assert orc.exp_approx(-10.5) == 0.0
+    assert orc.exp_approx(10.5) == 22026.0
+    assert orc.exp_approx(-3.0) == 0.0  # the polynomial is negative there -> clamped
+    assert orc.exp_approx(float("nan")) == pytest.approx(exp_poly64(5.0), rel=1e-6)  # clamp returns 5
+    for v in np.linspace(-9.5, 9.5, 77):
+        assert orc.exp_approx(float(v)) == pytest.approx(exp_poly64(float(v)), rel=1e-5, abs=1e-5)
+
+
+@needs_ref
+@pytest.mark.parametrize("N", [1, 5, 8, 24, 29, 4096, 14336])
+def test_silu_softmax_vs_reference_build(N):
+    rng = orc.rng_for(35, N)
+    x = (rng.random(N, dtype=np.float32) * 24 - 12).astype(np.float32)
+    rc, yr = orc.ref_silu(x)
+    assert rc == 0 and same_bits(orc.silu(x), yr)
+    rc, yr = orc.ref_softmax(x)
+    assert rc == 0 and same_bits(orc.softmax(x), yr)
+
+
+def test_softmax_properties():
+    rng = orc.rng_for(36)
+    x = orc.gen_f32(2048, rng)
+    y = orc.softmax(x)
+    assert abs(float(np.sum(y, dtype=np.float64)) - 1.0) < 1e-5
+    assert np.argmax(y) == np.argmax(x)
+    assert np.all(y[x < x.max() - 2.2] == 0.0)  # the polynomial zeroes far scores
+    u = orc.softmax(np.full(64, 3.5, np.float32))
+    assert np.all(u == u[0]) and abs(u[0] - 1 / 64) < 1e-7
+
+
+@needs_ref
+def test_add_mul_vs_reference_build():
+    rng = orc.rng_for(37)
+    a, b = orc.gen_f32(1000, rng), orc.gen_f32(1000, rng)
+    rc, r = orc.ref_binary("q_add_f32_avx2", a, b)
+    assert rc == 0 and same_bits(orc.add(a, b), r)
+    rc, r = orc.ref_binary("q_mul_f32_avx2", a, b)
+    assert rc == 0 and same_bits(orc.mul(a, b), r)
+
+
+def test_argmax_first_index_on_ties():
+    x = np.array([1, 5, 5, 2, 5], np.float32)
+    assert orc.argmax(x) == 1
+    x = np.array([-np.inf, -np.inf], np.float32)
+    assert orc.argmax(x) == 0
+    rng = orc.rng_for(38)
+    y = orc.gen_f32(128256, rng)
+    assert orc.argmax(y) == int(np.argmax(y))
+
+
+@needs_ref
+@pytest.mark.parametrize("M,K,N", [(1, 128, 37), (1, 2048, 128), (3, 45, 7), (2, 32, 33)])
+def test_dot_order_vs_reference_matmul(M, K, N):
+    rng = orc.rng_for(39, K)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = rng.standard_normal((K, N), dtype=np.float32)
+    rc, Cr = orc.ref_matmul(A, B)
+    assert rc == 0
+    assert same_bits(orc.matmul_f32(A, B), Cr)
+
+
+# -------------------------------------------------------------- attention --
+
+def softmax_exp64(d):
+    """exp used by the reference softmax for a row of shifted scores d: the
+    polynomial on the first len&~7 entries, libm exp on the N%8 tail
+    (reference softmax.c:182-196); libm exp throughout when N < 8."""
+    n = len(d)
+    nv = n & ~7 if n >= 8 else 0
+    return np.array([exp_poly64(v) if i < nv else math.exp(v) for i, v in enumerate(d)])
+
+
+def attention64(q, kv, n_heads, n_kv, hd, max_seq, pos):
+    """Textbook decode attention in float64 with the reference softmax's exp."""
+    out = np.zeros(n_heads * hd)
+    S = pos + 1
+    for h in range(n_heads):
+        kvh = h // (n_heads // n_kv)
+        K = kv[kvh, :S, 0, :].astype(np.float64)
+        V = kv[kvh, :S, 1, :].astype(np.float64)
+        s = K @ q[h * hd:(h + 1) * hd].astype(np.float64) / math.sqrt(hd)
+        e = softmax_exp64(s - s.max())
+        out[h * hd:(h + 1) * hd] = (e / e.sum()) @ V
+    return out
+
+
+def test_attention_decode_vs_fp64():
+    rng = orc.rng_for(41)
+    n_heads, n_kv, hd, max_seq, pos = 8, 2, 128, 80, 70
+    kv = rng.standard_normal((n_kv, max_seq, 2, hd), dtype=np.float32)
+    q = rng.standard_normal(n_heads * hd, dtype=np.float32) * 0.3
+    got = orc.attention_decode(q, kv, n_heads, n_kv, hd, max_seq, pos)
+    want = attention64(q, kv, n_heads, n_kv, hd, max_seq, pos)
+    assert np.max(np.abs(got - want)) < 1e-4
+
+
+def test_attention_gqa_mapping_and_causality():
+    n_heads, n_kv, hd, max_seq, pos = 8, 2, 128, 16, 9
+    kv = np.zeros((n_kv, max_seq, 2, hd), np.float32)
+    kv[1, :, 1, :] = 1.0            # only kv head 1 has non-zero values
+    kv[0, pos + 1:, 1, :] = 100.0   # beyond pos: must never be read
+    q = np.zeros(n_heads * hd, np.float32)
+    out = orc.attention_decode(q, kv, n_heads, n_kv, hd, max_seq, pos).reshape(n_heads, hd)
+    assert np.all(out[:4] == 0.0) and np.allclose(out[4:], 1.0)
