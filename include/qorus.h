@@ -102,6 +102,30 @@ q_error_code q_silu_f32_avx2(const float* Q_RESTRICT x, float* Q_RESTRICT output
  * Replaces reference qorus.h:179-183 / src/ops/avx2/softmax.c:17-132. */
 q_error_code q_softmax_f32_avx2(const float* Q_RESTRICT x, float* Q_RESTRICT output, uint32_t N);
 
+/* ---- Llama-3 model (reference include/qorus.h:193-219) ---- */
+
+/* Build tensor views over the mapped model and the HBM decode plan.
+ * Replaces reference qorus.h:193-196 / src/models/model.c:294-673. */
+q_error_code llama_build_graph(q_context* Q_RESTRICT ctx, q_llama_model* Q_RESTRICT model);
+
+/* Replaces reference qorus.h:200 / src/models/model.c:675-691. */
+void llama_free_graph(q_llama_model* Q_RESTRICT model);
+
+/* Run tokens[0..seq_len) at positions pos.. and write the logits of the
+ * last token to the host buffer `logits` [vocab_size].
+ * Replaces reference qorus.h:212-219 / src/models/model.c:1655-1850. */
+q_error_code llama_forward(q_llama_model* Q_RESTRICT model, q_context* Q_RESTRICT ctx,
+                           const uint32_t* Q_RESTRICT tokens, uint32_t seq_len,
+                           uint32_t pos, float* Q_RESTRICT logits);
+
+/* Greedy (temperature < 1e-6) token selection: first index of the maximum.
+ * Sampling with temperature/top-k/top-p is not part of this build and
+ * returns Q_ERR_INVALID_ARG.
+ * Replaces reference qorus.h:292-300 / src/main.c:852-881. */
+q_error_code q_sample_token(const float* Q_RESTRICT logits, uint32_t vocab_size,
+                            float temperature, uint32_t top_k, float top_p,
+                            uint32_t* Q_RESTRICT token_id_out, q_context* Q_RESTRICT ctx);
+
 #ifdef __cplusplus
 }
 #endif

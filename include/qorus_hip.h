@@ -119,6 +119,20 @@ q_error_code qh_mul_f32(const float* a, const float* b, float* output, uint32_t 
  * maximum); writes the index to device memory *index_out. */
 q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_stream s);
 
+/* ---- Decode on the device ---- */
+
+/* Greedy generation with no host round trip between steps (no reference
+ * counterpart; it is the device form of the q_generate loop, reference
+ * src/main.c:994-1131, with temperature 0): n_steps decode steps of a model
+ * built by llama_build_graph, starting from `token` at position `pos`; each
+ * step's argmax becomes the next token and the position advances on the
+ * device.  tokens_out (host) receives the n_steps generated tokens and
+ * *ms_per_step (if non-NULL) the mean step time from HIP events around the
+ * replays of the captured step graph.  Requires pos + n_steps <= max_seq_len.
+ * The KV cache rows pos..pos+n_steps-1 are overwritten. */
+q_error_code qh_llama_generate(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
+                               uint32_t n_steps, uint32_t* tokens_out, float* ms_per_step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,7 @@
 #include <cstdint>
 
 #include "qh_kernels.hpp"
+#include "qh_digits.hpp"
 #include "qh_vec.hpp"
 
 namespace qh {
@@ -66,112 +67,50 @@ hipError_t launch_dequant(const uint8_t* blocks, float* out, uint64_t n_blocks, 
 }
 
 // ---------------------------------------------------------------------------
-// Digit-plane preparation of one 32-element block.
+// Digit planes of the GEMV input.  32 consecutive lanes own one 32-element
+// block (lane = element): block max and NaN/Inf flag by cross-lane
+// reductions, x_int = round(x * 2^k), its 6 balanced base-16 digits, and the
+// 8-lane OR that packs each plane dword.  Lanes 0..5 of each 8-lane group
+// store plane dwords, lanes 6..7 of the first group store (k, z).
 // ---------------------------------------------------------------------------
-constexpr int kDigitMax = 7829367;   // 7 * (16^6 - 1) / 15: largest 6-digit balanced value
-constexpr uint32_t kDigitBias = 8947848u;  // 8 * (16^6 - 1) / 15
+constexpr int kPrepThreads = 256;  // 8 blocks per pass
 
-__device__ inline void prep_block(const float (&v)[32], uint4 (&planes)[6], uint4& meta) {
-    float m = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-        const float a = fabsf(v[e]);
-        bad |= !(a <= FLT_MAX);  // NaN or infinity
-        m = fmaxf(m, a);
-    }
-    int k = 0;
-    if (!bad && m > 0.0f) {
-        const int E = __builtin_amdgcn_frexp_expf(m);  // m < 2^E
-        k = 23 - E;
-        if (rintf(ldexpf(m, k)) > (float)kDigitMax) k -= 1;
-    }
-    uint32_t pl[6][4];
-#pragma unroll
-    for (int p = 0; p < 6; ++p)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pl[p][i] = 0u;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-        const int xi = bad ? 0 : (int)rintf(ldexpf(v[e], k));
-        const uint32_t u = (uint32_t)(xi + (int)kDigitBias);  // 6 unsigned nibbles = digit + 8
-#pragma unroll
-        for (int p = 0; p < 6; ++p) pl[p][e >> 3] |= ((u >> (4 * p)) & 15u) << (4 * (e & 7));
-    }
-#pragma unroll
-    for (int p = 0; p < 6; ++p)
-        planes[p] = make_uint4(pl[p][0] ^ 0x88888888u, pl[p][1] ^ 0x88888888u,
-                               pl[p][2] ^ 0x88888888u, pl[p][3] ^ 0x88888888u);
-    const float z = bad ? __builtin_nanf("") : 0.0f;
-    meta = make_uint4((uint32_t)k, __float_as_uint(z), 0u, 0u);
+// Digits of x: one lane per element.
+__global__ __launch_bounds__(kPrepThreads) void k_xprep(const float* __restrict__ x, uint32_t nblk,
+                                                        uint32_t pad, uint32_t* __restrict__ xd) {
+    const uint32_t t = blockIdx.x * kPrepThreads + threadIdx.x;
+    const uint32_t c = t >> 5;
+    const bool valid = c < nblk;
+    const float v = valid ? x[t] : 0.0f;
+    prep_lane(v, c, valid, pad, xd);
 }
 
-__device__ inline void store_xd(uint4* __restrict__ xd, uint32_t pad, uint32_t c, const uint4 (&pl)[6],
-                                const uint4& meta) {
-#pragma unroll
-    for (int p = 0; p < 6; ++p) xd[(size_t)p * pad + c] = pl[p];
-    xd[(size_t)6 * pad + c] = meta;
-}
+// Fused RMSNorm + digits.  Every workgroup computes the same sum of squares
+// (identical fixed order, see rms_scale) and prepares its own 8*passes
+// blocks.  RMSNorm follows reference src/ops/avx2/rmsnorm.c:33-89 except for
+// the order of that sum: h = (x*r)*w, bit-identical to the standalone
+// RMSNorm kernel.
+constexpr uint32_t kNormPrepBlocksPerWg = 16;
 
-// Digits of x (no normalisation): one thread per block.
-__global__ __launch_bounds__(256) void k_xprep(const float* __restrict__ x, uint32_t nblk, uint32_t pad,
-                                               uint4* __restrict__ xd) {
-    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= pad) return;
-    uint4 pl[6], meta;
-    if (c < nblk) {
-        float v[32];
-        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)c * 32);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 t = xp[i];
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-        }
-        prep_block(v, pl, meta);
-    } else {
-        // Padding columns: all-zero digits (digit 0 is nibble 0) and k = 0.
-#pragma unroll
-        for (int p = 0; p < 6; ++p) pl[p] = make_uint4(0u, 0u, 0u, 0u);
-        meta = make_uint4(0u, 0u, 0u, 0u);
-    }
-    store_xd(xd, pad, c, pl, meta);
-}
-
-// Fused RMSNorm + digits, one workgroup.  RMSNorm follows reference
-// src/ops/avx2/rmsnorm.c:33-89 except for the order of the sum of squares
-// (a fixed tree here, 8 lane chains there): see rms_scale; h = (x*r)*w.
-// Produces the same bits as the standalone RMSNorm kernel.
-constexpr int kNormThreads = 1024;
-
-__global__ __launch_bounds__(kNormThreads) void k_norm_xprep(const float* __restrict__ x, uint32_t N,
+__global__ __launch_bounds__(kPrepThreads) void k_norm_xprep(const float* __restrict__ x, uint32_t N,
                                                              const float* __restrict__ w, float eps,
                                                              float* __restrict__ h_out, uint32_t pad,
-                                                             uint4* __restrict__ xd) {
-    __shared__ float red[kNormThreads / 64];
-    const uint32_t tid = threadIdx.x;
-    const float r = rms_scale<kNormThreads>(x, N, eps, red);
+                                                             uint32_t* __restrict__ xd) {
+    __shared__ float red[kPrepThreads / 64];
+    const float r = rms_scale<kPrepThreads>(x, N, eps, red);
     const uint32_t nblk = N / 32;
-    for (uint32_t c = tid; c < pad; c += kNormThreads) {
-        uint4 pl[6], meta;
-        if (c < nblk) {
-            float v[32];
 #pragma unroll
-            for (int e = 0; e < 32; ++e) {
-                const float n = x[(size_t)c * 32 + e] * r;
-                v[e] = n * w[(size_t)c * 32 + e];
-            }
-            if (h_out) {
-                float4* hp = reinterpret_cast<float4*>(h_out + (size_t)c * 32);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) hp[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-            }
-            prep_block(v, pl, meta);
-        } else {
-#pragma unroll
-            for (int p = 0; p < 6; ++p) pl[p] = make_uint4(0u, 0u, 0u, 0u);
-            meta = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t pass = 0; pass < kNormPrepBlocksPerWg / (kPrepThreads / 32); ++pass) {
+        const uint32_t t = (blockIdx.x * kNormPrepBlocksPerWg + pass * (kPrepThreads / 32)) * 32 + threadIdx.x;
+        const uint32_t c = t >> 5;
+        const bool valid = c < nblk;
+        float v = 0.0f;
+        if (valid) {
+            const float n = x[t] * r;
+            v = n * w[t];
+            if (h_out) h_out[t] = v;
         }
-        store_xd(xd, pad, c, pl, meta);
+        prep_lane(v, c, valid, pad, xd);
     }
 }
 
@@ -179,11 +118,14 @@ hipError_t launch_xprep(const float* x, uint32_t N, const float* norm_w, float e
                         uint4* xd, hipStream_t s) {
     const uint32_t nblk = N / 32;
     const uint32_t pad = xd_pad(nblk);
+    uint32_t* xdw = reinterpret_cast<uint32_t*>(xd);
     if (norm_w) {
-        hipLaunchKernelGGL(k_norm_xprep, dim3(1), dim3(kNormThreads), 0, s, x, N, norm_w, eps, h_out,
-                           pad, xd);
+        const uint32_t grid = (nblk + kNormPrepBlocksPerWg - 1) / kNormPrepBlocksPerWg;
+        hipLaunchKernelGGL(k_norm_xprep, dim3(grid), dim3(kPrepThreads), 0, s, x, N, norm_w, eps, h_out, pad,
+                           xdw);
     } else {
-        hipLaunchKernelGGL(k_xprep, dim3((pad + 255) / 256), dim3(256), 0, s, x, nblk, pad, xd);
+        const uint32_t grid = (nblk * 32 + kPrepThreads - 1) / kPrepThreads;
+        hipLaunchKernelGGL(k_xprep, dim3(grid), dim3(kPrepThreads), 0, s, x, nblk, pad, xdw);
     }
     return hipGetLastError();
 }
@@ -197,37 +139,30 @@ struct GemvArgs {
     const float* res[4];
     uint32_t M[4];
     uint32_t tile_end[4];  // cumulative workgroup counts per segment
+    uint32_t hd[4];        // decode epilogue (0: contiguous store)
+    uint32_t head_stride[4];
+    uint32_t pos_stride[4];
+    uint32_t rope_mask;    // bit i: segment i applies RoPE
     uint32_t nseg;
     uint32_t nblk;
     uint32_t pad;
     const uint4* xd;
+    const uint32_t* pos;
+    const float* cos_tab;
+    const float* sin_tab;
 };
 
-// Contribution of one block: ldexp(s * P, -k) with P the exact integer dot.
-__device__ inline float block_dot(const uint4 q, const float s, const uint4 (&xp)[6], const int k,
-                                  const float z) {
-    const int w0 = (int)(q.x ^ 0x88888888u), w1 = (int)(q.y ^ 0x88888888u);
-    const int w2 = (int)(q.z ^ 0x88888888u), w3 = (int)(q.w ^ 0x88888888u);
-    int a = 0;
-#pragma unroll
-    for (int p = 5; p >= 0; --p) {
-        if (p < 5) a <<= 4;
-        a = __builtin_amdgcn_sdot8(w0, (int)xp[p].x, a, false);
-        a = __builtin_amdgcn_sdot8(w1, (int)xp[p].y, a, false);
-        a = __builtin_amdgcn_sdot8(w2, (int)xp[p].z, a, false);
-        a = __builtin_amdgcn_sdot8(w3, (int)xp[p].w, a, false);
-    }
-    const float c = fmaf(s, (float)a, z);
-    return ldexpf(c, -k);
-}
-
-// W waves split K, G independent row groups per workgroup, RW rows per wave,
-// J block columns per lane per K-chunk (K-chunk = 64*W*J blocks).
-template <int W, int J, int G, int RW>
+// W waves split K, G independent row groups per workgroup, RW rows per wave
+// (processed R at a time, the next batch loaded while the current one is
+// computed), J block columns per lane per K-chunk (K-chunk = 64*W*J blocks).
+// Every load is unconditional: out-of-range rows/columns read a clamped,
+// in-bounds address and are masked (scale and digits zeroed), so the
+// compiler keeps all loads of a batch in flight together.
+template <int W, int J, int G, int RW, int R>
 __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
     constexpr int kChunk = 64 * W * J;
-    constexpr int R = 4;  // rows loaded per batch
-    static_assert(RW % R == 0, "RW must be a multiple of 4");
+    constexpr int NB = RW / R;
+    static_assert(RW % R == 0, "RW must be a multiple of R");
 
     // Segment of this workgroup (uniform).
     const uint32_t t = blockIdx.x;
@@ -254,46 +189,88 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
     for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
 
     for (uint32_t cb = 0; cb < a.nblk; cb += kChunk) {
-        uint4 xp[J][6];
-        int kk[J];
-        float zz[J];
-        uint32_t col[J];
+        uint32_t coff[J];
         bool ok[J];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            col[j] = cb + (uint32_t)((j * W + kw) * 64 + lane);
-            ok[j] = col[j] < a.nblk;
-            const uint32_t cc = ok[j] ? col[j] : 0u;
-#pragma unroll
-            for (int p = 0; p < 6; ++p) xp[j][p] = a.xd[(size_t)p * a.pad + cc];
-            const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
-            kk[j] = (int)meta.x;
-            zz[j] = __uint_as_float(meta.y);
+            const uint32_t col = cb + (uint32_t)((j * W + kw) * 64 + lane);
+            ok[j] = col < a.nblk;
+            coff[j] = (ok[j] ? col : 0u) * 20u;
         }
-#pragma unroll
-        for (int rb = 0; rb < RW; rb += R) {
-            uint4 q[R][J];
-            float s[R][J];
+        uint4 q[2][R][J];
+        float s[2][R][J];
+        auto load_batch = [&](int b, int buf) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const uint32_t row = row0 + rb + r;
+                uint32_t row = row0 + (uint32_t)(b * R + r);
+                row = row < M ? row : M - 1u;
                 const uint8_t* rp = wseg + (size_t)row * row_bytes;
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    q[r][j] = make_uint4(0u, 0u, 0u, 0u);
-                    s[r][j] = 0.0f;
-                    if (row < M && ok[j]) {
-                        const uint8_t* bp = rp + (size_t)col[j] * 20u;
-                        q[r][j] = *reinterpret_cast<const uint4*>(__builtin_assume_aligned(bp, 4));
-                        s[r][j] = *reinterpret_cast<const float*>(__builtin_assume_aligned(bp + 16, 4));
-                    }
+                    const uint8_t* bp = rp + coff[j];
+                    q[buf][r][j] = *reinterpret_cast<const uint4*>(__builtin_assume_aligned(bp, 4));
+                    s[buf][r][j] = *reinterpret_cast<const float*>(__builtin_assume_aligned(bp + 16, 4));
                 }
             }
+        };
+        load_batch(0, 0);
+
+        uint4 xp[J][6];
+        int kk[J];
+        float zz[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t cc = coff[j] / 20u;
+#pragma unroll
+            for (int p = 0; p < 6; ++p) {
+                const uint4 v = a.xd[(size_t)p * a.pad + cc];
+                xp[j][p] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
+            }
+            const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
+            kk[j] = ok[j] ? (int)meta.x : 0;
+            zz[j] = ok[j] ? __uint_as_float(meta.y) : 0.0f;
+        }
+
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b + 1 < NB) load_batch(b + 1, (b + 1) & 1);
+            // Integer dots of the R*J blocks of this batch, plane by plane
+            // across all blocks: each plane is a 4-deep dot8 chain of its
+            // own and the planes combine by P = (P << 4) + S_p, so the
+            // independent chains of different blocks interleave.
+            int P[R][J];
+            uint32_t wq[R][J][4];
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int j = 0; j < J; ++j)
-                    if (ok[j]) acc[rb + r] += block_dot(q[r][j], s[r][j], xp[j], kk[j], zz[j]);
+                for (int j = 0; j < J; ++j) {
+                    const uint4 qq = q[b & 1][r][j];
+                    wq[r][j][0] = qq.x ^ 0x88888888u;
+                    wq[r][j][1] = qq.y ^ 0x88888888u;
+                    wq[r][j][2] = qq.z ^ 0x88888888u;
+                    wq[r][j][3] = qq.w ^ 0x88888888u;
+                    P[r][j] = 0;
+                }
+#pragma unroll
+            for (int p = 5; p >= 0; --p)
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int j = 0; j < J; ++j) {
+                        int sp = __builtin_amdgcn_sdot8((int)wq[r][j][0], (int)xp[j][p].x, 0, false);
+                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][1], (int)xp[j][p].y, sp, false);
+                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][2], (int)xp[j][p].z, sp, false);
+                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][3], (int)xp[j][p].w, sp, false);
+                        P[r][j] = (int)((uint32_t)P[r][j] << 4) + sp;
+                    }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const float sc = ok[j] ? s[b & 1][r][j] : 0.0f;
+                    const float c = fmaf(sc, (float)P[r][j], zz[j]);
+                    acc[b * R + r] += ldexpf(c, -kk[j]);
+                }
         }
     }
 
@@ -309,12 +286,28 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
     const float* __restrict__ res = a.res[sg];
     if constexpr (W == 1) {
         if (lane < RW) {
-            float v = 0.0f;
+            float v = acc[0], pv = acc[1];
 #pragma unroll
-            for (int r = 0; r < RW; ++r)
-                if (r == lane) v = acc[r];
+            for (int r = 1; r < RW; ++r) v = (r == lane) ? acc[r] : v;
+#pragma unroll
+            for (int r = 0; r < RW; ++r) pv = (r == (lane ^ 1)) ? acc[r] : pv;
             const uint32_t row = row0 + lane;
-            if (row < M) y[row] = res ? res[row] + v : v;
+            const uint32_t hd = a.hd[sg];
+            float* dst = y + row;
+            if (hd) {
+                const uint32_t pos = *a.pos;
+                const uint32_t i = row % hd;
+                if ((a.rope_mask >> sg) & 1u) {
+                    // Pair (x0, x1) = (row&~1, row|1): y0 = x0*c - x1*s,
+                    // y1 = x1*c + x0*s, products rounded separately.
+                    const float c = a.cos_tab[(size_t)pos * hd + i];
+                    const float sn = a.sin_tab[(size_t)pos * hd + i];
+                    const float t0 = v * c, t1 = pv * sn;
+                    v = (lane & 1) ? t0 + t1 : t0 - t1;
+                }
+                dst = y + (size_t)pos * a.pos_stride[sg] + (size_t)(row / hd) * a.head_stride[sg] + i;
+            }
+            if (row < M) *dst = res ? res[row] + v : v;
         }
     } else {
         __shared__ float red[G][W][RW];
@@ -335,8 +328,9 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
     }
 }
 
-template <int W, int J, int G, int RW>
-static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s) {
+template <int W, int J, int G, int RW, int R>
+static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
+                           const GemvDecode* dec) {
     GemvArgs a{};
     constexpr uint32_t tile_rows = G * RW;
     uint32_t tiles = 0;
@@ -346,6 +340,14 @@ static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const u
             a.y[i] = segs[i].y;
             a.res[i] = segs[i].res;
             a.M[i] = segs[i].M;
+            a.hd[i] = segs[i].hd;
+            a.head_stride[i] = segs[i].head_stride;
+            a.pos_stride[i] = segs[i].pos_stride;
+            if (segs[i].rope) a.rope_mask |= 1u << i;
+            // The decode epilogue exists on the single-wave-per-row path only,
+            // and RoPE needs whole pairs inside one wave's rows.
+            if (segs[i].hd && (W != 1 || !dec || !dec->pos || (segs[i].hd % 2) != 0)) return hipErrorInvalidValue;
+            if (segs[i].rope && (!dec->cos_tab || !dec->sin_tab || (RW % 2) != 0)) return hipErrorInvalidValue;
             tiles += (segs[i].M + tile_rows - 1) / tile_rows;
         }
         a.tile_end[i] = tiles;
@@ -354,17 +356,32 @@ static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const u
     a.nblk = nblk;
     a.pad = xd_pad(nblk);
     a.xd = xd;
+    if (dec) {
+        a.pos = dec->pos;
+        a.cos_tab = dec->cos_tab;
+        a.sin_tab = dec->sin_tab;
+    }
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_gemv<W, J, G, RW>), dim3(tiles), dim3(64 * W * G), 0, s, a);
+    hipLaunchKernelGGL((k_gemv<W, J, G, RW, R>), dim3(tiles), dim3(64 * W * G), 0, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s) {
+// Launch shape by input width (nblk = N/32 blocks) and total rows.
+hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
+                       const GemvDecode* dec) {
     if (nseg < 1 || nseg > 4) return hipErrorInvalidValue;
-    if (nblk <= 64) return run_gemv<1, 1, 4, 4>(segs, nseg, nblk, xd, s);
-    if (nblk <= 128) return run_gemv<1, 2, 4, 4>(segs, nseg, nblk, xd, s);
-    if (nblk <= 256) return run_gemv<2, 2, 2, 8>(segs, nseg, nblk, xd, s);
-    return run_gemv<4, 2, 1, 16>(segs, nseg, nblk, xd, s);
+    uint64_t rows = 0;
+    for (int i = 0; i < nseg; ++i) rows += segs[i].M;
+    const bool many_rows = rows >= 16384;
+    if (nblk <= 64) return run_gemv<1, 1, 4, 4, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 128) {
+        if (many_rows) return run_gemv<1, 2, 4, 8, 4>(segs, nseg, nblk, xd, s, dec);
+        return run_gemv<1, 2, 4, 4, 4>(segs, nseg, nblk, xd, s, dec);
+    }
+    if (nblk <= 256) return run_gemv<2, 2, 2, 8, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 448) return run_gemv<7, 1, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 512) return run_gemv<8, 1, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
+    return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
 }
 
 }  // namespace qh

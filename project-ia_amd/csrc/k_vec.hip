@@ -21,20 +21,24 @@ namespace qh {
 
 constexpr int kVecThreads = 1024;
 
-// RMSNorm, one workgroup: y = (x*r)*w (reference src/ops/avx2/rmsnorm.c:166-176).
-__global__ __launch_bounds__(kVecThreads) void k_rmsnorm(const float* __restrict__ x,
-                                                         const float* __restrict__ w, float* __restrict__ y,
-                                                         uint32_t N, float eps) {
-    __shared__ float red[kVecThreads / 64];
-    const float r = rms_scale<kVecThreads>(x, N, eps, red);
-    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) {
+// RMSNorm, one workgroup of 256 threads: y = (x*r)*w (reference
+// src/ops/avx2/rmsnorm.c:166-176).  Same reduction as the fused
+// RMSNorm + digit-prep kernel, so both give identical bits.
+constexpr int kNormThreads = 256;
+
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm(const float* __restrict__ x,
+                                                          const float* __restrict__ w, float* __restrict__ y,
+                                                          uint32_t N, float eps) {
+    __shared__ float red[kNormThreads / 64];
+    const float r = rms_scale<kNormThreads>(x, N, eps, red);
+    for (uint32_t i = threadIdx.x; i < N; i += kNormThreads) {
         const float n = x[i] * r;
         y[i] = n * w[i];
     }
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kVecThreads), 0, s, x, w, y, N, eps);
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), 0, s, x, w, y, N, eps);
     return hipGetLastError();
 }
 
@@ -157,8 +161,12 @@ __device__ __forceinline__ bool arg_better(float v, uint32_t i, float bv, uint32
     return v > bv || (v == bv && i < bi);
 }
 
+// With pos_inout / hist (the on-device generation loop): also advance the
+// position and append the token to hist[0..hist_cap).
 __global__ __launch_bounds__(kVecThreads) void k_argmax(const float* __restrict__ x, uint32_t N,
-                                                        uint32_t* __restrict__ out) {
+                                                        uint32_t* __restrict__ out, uint32_t* __restrict__ pos_inout,
+                                                        uint32_t* __restrict__ hist, uint32_t* __restrict__ hist_n,
+                                                        uint32_t hist_cap) {
     __shared__ float sv[kVecThreads / 64];
     __shared__ uint32_t si[kVecThreads / 64];
     float bv = -INFINITY;
@@ -195,11 +203,23 @@ __global__ __launch_bounds__(kVecThreads) void k_argmax(const float* __restrict_
         if (N > 0 && x[0] != x[0]) i = 0;  // NaN at index 0: nothing compares greater
         if (i == 0xFFFFFFFFu) i = 0;
         *out = i;
+        if (pos_inout) *pos_inout += 1u;
+        if (hist) {
+            const uint32_t n = *hist_n;
+            if (n < hist_cap) hist[n] = i;
+            *hist_n = n + 1u;
+        }
     }
 }
 
 hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, out);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, out, nullptr, nullptr, nullptr, 0u);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_step(const float* x, uint32_t N, uint32_t* tok_out, uint32_t* pos_inout, uint32_t* hist,
+                              uint32_t* hist_n, uint32_t hist_cap, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, tok_out, pos_inout, hist, hist_n, hist_cap);
     return hipGetLastError();
 }
 

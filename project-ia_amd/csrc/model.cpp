@@ -1,8 +1,572 @@
-// model.cpp -- Llama-3 decode plan on MI355X (device state of a built model).
+// model.cpp -- Llama-3 decode on one MI355X behind the reference model API
+// (llama_build_graph / llama_forward / llama_free_graph / q_sample_token).
+//
+// Host side keeps the reference's data structures: tensor views and layer
+// structs in the q_context arena, pointing into the mapped .qorus file
+// (reference src/models/model.c:294-673).  The device plan lives in the
+// q_context side table: device addresses of every tensor (the HBM mirror
+// made by q_init_memory, same offsets), one HBM scratch arena allocated once
+// here (no allocation per token), RoPE tables for every position computed on
+// the host with the reference's libm calls and uploaded, and a captured HIP
+// graph of the whole decode step.  Token and position are read by the
+// kernels from device memory, so the one graph serves every step and a
+// generation loop can feed the greedy token back on the device.
+//
+// Model file: .qorus version 3 (shapes [out, in] as the GEMV consumes them,
+// Q4_0 LM head); see qorus_amd/model_file.py.  The reference's own writer
+// stores FP32 bytes in Q4_0 slots and [in, out] shapes, which its forward
+// cannot run at Llama-3 shapes; those files are rejected with
+// Q_ERR_INVALID_CONFIG.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "qh_decode.hpp"
+#include "qh_kernels.hpp"
 #include "qh_runtime.hpp"
 
 namespace qh {
 
-void plan_destroy(CtxState* st) { st->plan = nullptr; }
+hipError_t launch_argmax_step(const float* x, uint32_t N, uint32_t* tok_out, uint32_t* pos_inout,
+                              uint32_t* hist, uint32_t* hist_n, uint32_t hist_cap, hipStream_t s);  // k_vec.hip
+
+struct LayerDev {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *attn_norm, *ffn_norm;
+};
+
+struct ModelPlan {
+    const q_llama_model* model = nullptr;
+    q_llama_config cfg{};
+    uint32_t hd = 0, kvd = 0;
+    float scale = 0.0f;
+    const float* embd = nullptr;
+    const float* out_norm = nullptr;
+    const uint8_t* lm_head = nullptr;
+    std::vector<LayerDev> layers;
+    // HBM scratch arena (one allocation)
+    uint8_t* arena = nullptr;
+    size_t arena_bytes = 0;
+    float *x = nullptr, *x1 = nullptr, *q = nullptr, *g = nullptr, *u = nullptr, *logits = nullptr;
+    uint4 *xd_a = nullptr, *xd_b = nullptr, *xd_c = nullptr;
+    float *scores = nullptr, *part_max = nullptr, *part_sum = nullptr, *o_part = nullptr;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+    uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
+    uint32_t hist_cap = 0;
+    float* kv = nullptr;
+    size_t kv_layer_floats = 0;
+    hipStream_t stream = nullptr;
+    hipGraphExec_t step_graph = nullptr;     // decode step, host-fed token/pos
+    hipGraphExec_t gen_graph = nullptr;      // decode step + greedy feedback + pos advance
+    uint32_t* pinned = nullptr;              // host staging for token/pos
+};
+
+static std::mutex g_plan_mu;
+
+void plan_destroy(CtxState* st) {
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    ModelPlan* p = static_cast<ModelPlan*>(st->plan);
+    if (!p) return;
+    if (p->stream) (void)hipStreamSynchronize(p->stream);
+    if (p->step_graph) (void)hipGraphExecDestroy(p->step_graph);
+    if (p->gen_graph) (void)hipGraphExecDestroy(p->gen_graph);
+    if (p->arena) (void)hipFree(p->arena);
+    if (p->pinned) (void)hipHostFree(p->pinned);
+    if (p->stream) (void)hipStreamDestroy(p->stream);
+    delete p;
+    st->plan = nullptr;
+    st->dev_arena = nullptr;
+    st->dev_arena_size = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side views (reference create_tensor_view, model.c:170-292)
+// ---------------------------------------------------------------------------
+static bool mul_ok(size_t a, size_t b, size_t* out) {
+    if (a != 0 && b > SIZE_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+static size_t f32_bytes(uint32_t n0, uint32_t n1) {
+    size_t s;
+    if (!mul_ok(n0, n1, &s) || !mul_ok(s, 4, &s)) return 0;
+    return s;
+}
+
+static size_t q4_bytes(uint32_t rows, uint32_t cols) {
+    if (cols % 32 != 0) return 0;
+    size_t s;
+    if (!mul_ok(rows, cols / 32, &s) || !mul_ok(s, sizeof(q_block_q4_0), &s)) return 0;
+    return s;
+}
+
+static q_tensor* make_view(q_context* ctx, size_t offset, uint32_t n0, uint32_t n1, q_dtype type, const char* name) {
+    q_tensor* t = static_cast<q_tensor*>(q_arena_alloc(ctx, sizeof(q_tensor)));
+    if (!t) return nullptr;
+    std::memset(t, 0, sizeof(*t));
+    t->data = static_cast<uint8_t*>(ctx->weights_mmap) + offset;
+    t->scales = nullptr;
+    t->ne[0] = n0;
+    t->ne[1] = n1;
+    t->ne[2] = 1;
+    t->ne[3] = 1;
+    t->type = type;
+    if (type == Q_F32) {
+        t->nb[3] = 4;
+        t->nb[2] = 4;
+        t->nb[1] = 4;
+        t->nb[0] = (size_t)n1 * 4;
+    } else {
+        t->nb[0] = (size_t)(n1 / 32) * sizeof(q_block_q4_0);
+        t->nb[1] = t->nb[2] = t->nb[3] = sizeof(q_block_q4_0);
+    }
+    std::strncpy(t->name, name, sizeof(t->name) - 1);
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// Decode step enqueue (all kernels on p->stream)
+// ---------------------------------------------------------------------------
+static hipError_t enqueue_step(ModelPlan* p, bool feedback) {
+    const q_llama_config& c = p->cfg;
+    hipStream_t s = p->stream;
+    hipError_t e;
+#define QH_E(x)                          \
+    do {                                 \
+        e = (x);                         \
+        if (e != hipSuccess) return e;   \
+    } while (0)
+    QH_E(launch_embed(p->embd, p->tok, c.vocab_size, c.dim, p->x, s));
+    GemvDecode dec;
+    dec.pos = p->pos;
+    dec.cos_tab = p->cos_tab;
+    dec.sin_tab = p->sin_tab;
+    const uint32_t nblk_d = c.dim / 32, nblk_h = c.hidden_dim / 32;
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const LayerDev& L = p->layers[l];
+        float* kvl = p->kv + (size_t)l * p->kv_layer_floats;
+        // attention block
+        QH_E(launch_xprep(p->x, c.dim, L.attn_norm, c.rms_norm_eps, nullptr, p->xd_a, s));
+        GemvSeg qkv[3];
+        qkv[0] = GemvSeg{L.wq, p->q, nullptr, c.dim};
+        qkv[0].hd = p->hd;
+        qkv[0].head_stride = p->hd;
+        qkv[0].rope = true;
+        qkv[1] = GemvSeg{L.wk, kvl, nullptr, p->kvd};
+        qkv[1].hd = p->hd;
+        qkv[1].head_stride = c.max_seq_len * 2 * p->hd;
+        qkv[1].pos_stride = 2 * p->hd;
+        qkv[1].rope = true;
+        qkv[2] = GemvSeg{L.wv, kvl + p->hd, nullptr, p->kvd};
+        qkv[2].hd = p->hd;
+        qkv[2].head_stride = c.max_seq_len * 2 * p->hd;
+        qkv[2].pos_stride = 2 * p->hd;
+        QH_E(launch_gemv(qkv, 3, nblk_d, p->xd_a, s, &dec));
+        AttnArgs aa;
+        aa.q = p->q;
+        aa.kv_layer = kvl;
+        aa.pos = p->pos;
+        aa.n_heads = c.n_heads;
+        aa.n_kv = c.n_kv_heads;
+        aa.head_dim = p->hd;
+        aa.max_seq = c.max_seq_len;
+        aa.scale = p->scale;
+        aa.scores = p->scores;
+        aa.part_max = p->part_max;
+        aa.part_sum = p->part_sum;
+        aa.o_part = p->o_part;
+        aa.o_out = nullptr;
+        aa.xd_out = p->xd_b;
+        QH_E(launch_attention(aa, s));
+        GemvSeg wo{L.wo, p->x1, p->x, c.dim};
+        QH_E(launch_gemv(&wo, 1, nblk_d, p->xd_b, s));
+        // MLP block
+        QH_E(launch_xprep(p->x1, c.dim, L.ffn_norm, c.rms_norm_eps, nullptr, p->xd_a, s));
+        GemvSeg gu[2] = {GemvSeg{L.wg, p->g, nullptr, c.hidden_dim}, GemvSeg{L.wu, p->u, nullptr, c.hidden_dim}};
+        QH_E(launch_gemv(gu, 2, nblk_d, p->xd_a, s));
+        QH_E(launch_swiglu_prep(p->g, p->u, c.hidden_dim, nullptr, p->xd_c, s));
+        GemvSeg wd{L.wd, p->x, p->x1, c.dim};
+        QH_E(launch_gemv(&wd, 1, nblk_h, p->xd_c, s));
+    }
+    QH_E(launch_xprep(p->x, c.dim, p->out_norm, c.rms_norm_eps, nullptr, p->xd_a, s));
+    GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
+    QH_E(launch_gemv(&lm, 1, nblk_d, p->xd_a, s));
+    if (feedback) QH_E(launch_argmax_step(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, s));
+#undef QH_E
+    return hipSuccess;
+}
+
+static q_error_code capture(ModelPlan* p, bool feedback, hipGraphExec_t* out) {
+    QH_TRY(hipStreamBeginCapture(p->stream, hipStreamCaptureModeThreadLocal));
+    const hipError_t e = enqueue_step(p, feedback);
+    hipGraph_t g = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(p->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(e, "decode step capture");
+    }
+    if (e2 != hipSuccess) return fail(e2, "hipStreamEndCapture");
+    const hipError_t e3 = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e3 != hipSuccess) return fail(e3, "hipGraphInstantiate");
+    return Q_OK;
+}
+
+static ModelPlan* plan_of(const q_llama_model* model, q_context* ctx) {
+    CtxState* st = ctx_state(ctx, false);
+    if (!st || !st->plan) return nullptr;
+    ModelPlan* p = static_cast<ModelPlan*>(st->plan);
+    return p->model == model ? p : nullptr;
+}
+
+static q_error_code check_kv(const ModelPlan* p, const q_context* ctx) {
+    const size_t need = (size_t)p->cfg.n_layers * p->kv_layer_floats * sizeof(float);
+    if (!ctx->kv_buffer || ctx->kv_size < need) return Q_ERR_INVALID_ARG;
+    return Q_OK;
+}
+
+// The captured graphs embed the KV-cache address: re-capture if it moved.
+static q_error_code bind_kv(ModelPlan* p, const q_context* ctx) {
+    float* kv = static_cast<float*>(ctx->kv_buffer);
+    if (p->kv != kv) {
+        QH_TRY(hipStreamSynchronize(p->stream));
+        if (p->step_graph) QH_TRY(hipGraphExecDestroy(p->step_graph));
+        if (p->gen_graph) QH_TRY(hipGraphExecDestroy(p->gen_graph));
+        p->step_graph = p->gen_graph = nullptr;
+        p->kv = kv;
+    }
+    return Q_OK;
+}
 
 }  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+// Reference src/models/model.c:294-673 (validation order kept; version-3
+// layout; the device plan added at the end).
+q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __restrict__ model) {
+    if (!ctx || !model) return Q_ERR_NULL_PTR;
+    if (!ctx->weights_mmap || !ctx->header) return Q_ERR_NULL_PTR;
+    const q_model_header* h = ctx->header;
+    if (h->magic != Q_MAGIC) return Q_ERR_INVALID_MAGIC;
+    if (h->n_layers == 0 || h->dim == 0 || h->vocab_size == 0 || h->n_heads == 0 || h->n_kv_heads == 0)
+        return Q_ERR_INVALID_CONFIG;
+    if (h->dim % 32 != 0 || h->hidden_dim % 32 != 0) return Q_ERR_INVALID_CONFIG;
+    // This build: version-3 layout, GQA group dividing the heads, 128-wide heads.
+    if (h->version < 3 || h->hidden_dim == 0 || h->max_seq_len == 0) return Q_ERR_INVALID_CONFIG;
+    if (h->n_heads % h->n_kv_heads != 0 || h->dim % h->n_heads != 0 || h->dim / h->n_heads != 128)
+        return Q_ERR_INVALID_CONFIG;
+    CtxState* st = ctx_state(ctx, false);
+    if (!st || !st->dev_weights) return Q_ERR_INVALID_ARG;  // not loaded by q_init_memory
+
+    q_llama_config& cfg = model->config;
+    cfg.vocab_size = h->vocab_size;
+    cfg.dim = h->dim;
+    cfg.hidden_dim = h->hidden_dim;
+    cfg.n_layers = h->n_layers;
+    cfg.n_heads = h->n_heads;
+    cfg.n_kv_heads = h->n_kv_heads;
+    cfg.max_seq_len = h->max_seq_len;
+    cfg.rope_freq_base = h->rope_freq_base;
+    cfg.rms_norm_eps = (h->version >= 2 && h->rms_norm_eps > 0.0f) ? h->rms_norm_eps : 1e-5f;
+    model->ctx = ctx;
+    const uint32_t hd = cfg.dim / cfg.n_heads;
+    const uint32_t kvd = cfg.n_kv_heads * hd;
+
+    // Tensor walk in file order, each tensor padded to 64 bytes.
+    size_t off = Q_HEADER_SIZE;
+    auto place = [&](size_t bytes, size_t* at) -> bool {
+        if (bytes == 0) return false;
+        const size_t al = Q_ALIGN_SIZE(bytes);
+        if (al < bytes || off > ctx->weights_size || al > ctx->weights_size - off) return false;
+        *at = off;
+        off += al;
+        return true;
+    };
+    size_t o;
+    if (!place(f32_bytes(cfg.vocab_size, cfg.dim), &o)) return Q_ERR_INVALID_CONFIG;
+    if (!(model->token_embd = make_view(ctx, o, cfg.vocab_size, cfg.dim, Q_F32, "token_embd.weight")))
+        return Q_ERR_ARENA_OOM;
+    if (!place(f32_bytes(cfg.dim, 1), &o)) return Q_ERR_INVALID_CONFIG;
+    if (!(model->output_norm = make_view(ctx, o, cfg.dim, 1, Q_F32, "output_norm.weight"))) return Q_ERR_ARENA_OOM;
+    if (!place(q4_bytes(cfg.vocab_size, cfg.dim), &o)) return Q_ERR_INVALID_CONFIG;
+    if (!(model->output = make_view(ctx, o, cfg.vocab_size, cfg.dim, Q_Q4_0, "output.weight")))
+        return Q_ERR_ARENA_OOM;
+    model->layers = static_cast<q_llama_layer*>(q_arena_alloc(ctx, sizeof(q_llama_layer) * cfg.n_layers));
+    if (!model->layers) return Q_ERR_ARENA_OOM;
+    struct Spec {
+        q_tensor** slot;
+        uint32_t n0, n1;
+        q_dtype type;
+        const char* name;
+    };
+    for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+        q_llama_layer* L = &model->layers[l];
+        std::memset(L, 0, sizeof(*L));
+        L->layer_idx = l;
+        const Spec specs[9] = {
+            {&L->attn_norm, cfg.dim, 1, Q_F32, "attn_norm.weight"},
+            {&L->wq, cfg.dim, cfg.dim, Q_Q4_0, "wq.weight"},
+            {&L->wk, kvd, cfg.dim, Q_Q4_0, "wk.weight"},
+            {&L->wv, kvd, cfg.dim, Q_Q4_0, "wv.weight"},
+            {&L->wo, cfg.dim, cfg.dim, Q_Q4_0, "wo.weight"},
+            {&L->ffn_norm, cfg.dim, 1, Q_F32, "ffn_norm.weight"},
+            {&L->w_gate, cfg.hidden_dim, cfg.dim, Q_Q4_0, "w_gate.weight"},
+            {&L->w_up, cfg.hidden_dim, cfg.dim, Q_Q4_0, "w_up.weight"},
+            {&L->w_down, cfg.dim, cfg.hidden_dim, Q_Q4_0, "w_down.weight"},
+        };
+        for (const Spec& sp : specs) {
+            const size_t bytes = sp.type == Q_F32 ? f32_bytes(sp.n0, sp.n1) : q4_bytes(sp.n0, sp.n1);
+            if (!place(bytes, &o)) return Q_ERR_INVALID_CONFIG;
+            if (!(*sp.slot = make_view(ctx, o, sp.n0, sp.n1, sp.type, sp.name))) return Q_ERR_ARENA_OOM;
+        }
+    }
+
+    // RoPE (reference model.c:625-665): freq_i = powf(base, -2i/hd), tables
+    // theta = freq_i * (float)pos through cosf/sinf, pairs duplicated.
+    const uint32_t pairs = hd / 2;
+    model->rope_freqs = static_cast<float*>(q_arena_alloc(ctx, pairs * sizeof(float)));
+    if (!model->rope_freqs) return Q_ERR_ARENA_OOM;
+    for (uint32_t i = 0; i < pairs; ++i) {
+        const float fe = -2.0f * (float)i / (float)hd;
+        model->rope_freqs[i] = powf(cfg.rope_freq_base, fe);
+    }
+    const size_t tab = (size_t)cfg.max_seq_len * hd;
+    std::vector<float> heap_cos, heap_sin;
+    float* ct = nullptr;
+    float* sn = nullptr;
+    model->rope_cache_enabled = false;
+    model->rope_cos_cache = model->rope_sin_cache = nullptr;
+    if (cfg.max_seq_len <= 8192) {
+        model->rope_cos_cache = static_cast<float*>(q_arena_alloc(ctx, tab * sizeof(float)));
+        model->rope_sin_cache = static_cast<float*>(q_arena_alloc(ctx, tab * sizeof(float)));
+        if (model->rope_cos_cache && model->rope_sin_cache) model->rope_cache_enabled = true;
+    }
+    if (model->rope_cache_enabled) {
+        ct = model->rope_cos_cache;
+        sn = model->rope_sin_cache;
+    } else {
+        heap_cos.resize(tab);
+        heap_sin.resize(tab);
+        ct = heap_cos.data();
+        sn = heap_sin.data();
+    }
+    for (uint32_t ps = 0; ps < cfg.max_seq_len; ++ps)
+        for (uint32_t i = 0; i < pairs; ++i) {
+            const float th = model->rope_freqs[i] * (float)ps;
+            const float cv = cosf(th), sv = sinf(th);
+            const size_t b = (size_t)ps * hd + 2 * i;
+            ct[b] = cv;
+            ct[b + 1] = cv;
+            sn[b] = sv;
+            sn[b + 1] = sv;
+        }
+    ctx->scratch_base_offset = ctx->scratch_head;
+
+    // ---- device plan ----
+    plan_destroy(st);
+    ModelPlan* p = new ModelPlan();
+    p->model = model;
+    p->cfg = cfg;
+    p->hd = hd;
+    p->kvd = kvd;
+    p->scale = 1.0f / sqrtf((float)hd);
+    auto dev = [&](const q_tensor* t) -> const uint8_t* {
+        return st->dev_weights + (static_cast<const uint8_t*>(t->data) - static_cast<const uint8_t*>(ctx->weights_mmap));
+    };
+    p->embd = reinterpret_cast<const float*>(dev(model->token_embd));
+    p->out_norm = reinterpret_cast<const float*>(dev(model->output_norm));
+    p->lm_head = dev(model->output);
+    for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+        const q_llama_layer& L = model->layers[l];
+        p->layers.push_back(LayerDev{dev(L.wq), dev(L.wk), dev(L.wv), dev(L.wo), dev(L.w_gate), dev(L.w_up),
+                                     dev(L.w_down), reinterpret_cast<const float*>(dev(L.attn_norm)),
+                                     reinterpret_cast<const float*>(dev(L.ffn_norm))});
+    }
+    p->kv_layer_floats = (size_t)cfg.n_kv_heads * cfg.max_seq_len * 2 * hd;
+    p->hist_cap = cfg.max_seq_len;
+    // HBM scratch arena layout (256-byte aligned pieces).
+    size_t bytes = 0;
+    auto carve = [&](size_t b) {
+        const size_t at = bytes;
+        bytes += (b + 255) & ~(size_t)255;
+        return at;
+    };
+    const size_t o_x = carve(cfg.dim * 4), o_x1 = carve(cfg.dim * 4), o_q = carve(cfg.dim * 4);
+    const size_t o_g = carve((size_t)cfg.hidden_dim * 4), o_u = carve((size_t)cfg.hidden_dim * 4);
+    const size_t o_lg = carve((size_t)cfg.vocab_size * 4);
+    const size_t o_xa = carve(xd_bytes(cfg.dim / 32)), o_xb = carve(xd_bytes(cfg.dim / 32));
+    const size_t o_xc = carve(xd_bytes(cfg.hidden_dim / 32));
+    const size_t nch = attention_n_chunks(cfg.max_seq_len);
+    const size_t o_sc = carve((size_t)cfg.n_heads * cfg.max_seq_len * 4);
+    const size_t o_pm = carve((size_t)cfg.n_heads * nch * 4), o_ps = carve((size_t)cfg.n_heads * nch * 4);
+    const size_t o_op = carve(nch * cfg.n_heads * hd * 4);
+    const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
+    const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
+    hipError_t e = hipMalloc(&p->arena, bytes);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        fail(e, "decode plan allocation");
+        st->plan = p;
+        plan_destroy(st);
+        return Q_ERR_ALLOC_FAILED;
+    }
+    p->arena_bytes = bytes;
+    uint8_t* A = p->arena;
+    p->x = reinterpret_cast<float*>(A + o_x);
+    p->x1 = reinterpret_cast<float*>(A + o_x1);
+    p->q = reinterpret_cast<float*>(A + o_q);
+    p->g = reinterpret_cast<float*>(A + o_g);
+    p->u = reinterpret_cast<float*>(A + o_u);
+    p->logits = reinterpret_cast<float*>(A + o_lg);
+    p->xd_a = reinterpret_cast<uint4*>(A + o_xa);
+    p->xd_b = reinterpret_cast<uint4*>(A + o_xb);
+    p->xd_c = reinterpret_cast<uint4*>(A + o_xc);
+    p->scores = reinterpret_cast<float*>(A + o_sc);
+    p->part_max = reinterpret_cast<float*>(A + o_pm);
+    p->part_sum = reinterpret_cast<float*>(A + o_ps);
+    p->o_part = reinterpret_cast<float*>(A + o_op);
+    p->cos_tab = reinterpret_cast<float*>(A + o_ct);
+    p->sin_tab = reinterpret_cast<float*>(A + o_st);
+    p->tok = reinterpret_cast<uint32_t*>(A + o_tok);
+    p->pos = reinterpret_cast<uint32_t*>(A + o_pos);
+    p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
+    p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
+    st->plan = p;
+    st->dev_arena = p->arena;
+    st->dev_arena_size = bytes;
+    e = hipMemset(p->arena, 0, bytes);
+    if (e == hipSuccess) e = hipMemcpy(p->cos_tab, ct, tab * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p->sin_tab, sn, tab * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        fail(e, "decode plan upload");
+        plan_destroy(st);
+        return Q_ERR_ALLOC_FAILED;
+    }
+    return Q_OK;
+}
+
+// Reference src/models/model.c:675-691 (plus the device plan).
+void llama_free_graph(q_llama_model* __restrict__ model) {
+    if (!model) return;
+    if (model->ctx) {
+        CtxState* st = ctx_state(model->ctx, false);
+        if (st && st->plan && static_cast<ModelPlan*>(st->plan)->model == model) plan_destroy(st);
+    }
+    model->token_embd = nullptr;
+    model->output_norm = nullptr;
+    model->output = nullptr;
+    model->layers = nullptr;
+    model->ctx = nullptr;
+    std::memset(&model->config, 0, sizeof(model->config));
+}
+
+// Reference src/models/model.c:1655-1850: tokens[0..seq_len) at positions
+// pos.., logits of the last token copied to the host buffer `logits`.
+// Tokens run one decode step each (causal attention over the cache).
+q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restrict__ ctx,
+                           const uint32_t* __restrict__ tokens, uint32_t seq_len, uint32_t pos,
+                           float* __restrict__ logits) {
+    if (!model || !ctx || !tokens || !logits) return Q_ERR_INVALID_ARG;
+    if (seq_len == 0) return Q_ERR_INVALID_SIZE;
+    if (seq_len > model->config.max_seq_len) return Q_ERR_INVALID_SIZE;
+    if (pos >= model->config.max_seq_len) return Q_ERR_INVALID_ARG;
+    if (!ctx->scratch_buffer) return Q_ERR_INVALID_ARG;
+    if (!ctx->kv_buffer) return Q_ERR_INVALID_ARG;
+    if ((uint64_t)pos + seq_len > model->config.max_seq_len) return Q_ERR_INVALID_ARG;
+    for (uint32_t t = 0; t < seq_len; ++t)
+        if (tokens[t] >= model->config.vocab_size) return Q_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    ModelPlan* p = plan_of(model, ctx);
+    if (!p) return Q_ERR_INVALID_ARG;
+    QH_TRY_CODE(check_kv(p, ctx));
+    QH_TRY_CODE(bind_kv(p, ctx));
+    if (!p->step_graph) QH_TRY_CODE(capture(p, false, &p->step_graph));
+    for (uint32_t t = 0; t < seq_len; ++t) {
+        QH_TRY(hipStreamSynchronize(p->stream));  // pinned staging is reused each step
+        p->pinned[0] = tokens[t];
+        p->pinned[1] = pos + t;
+        QH_TRY(hipMemcpyAsync(p->tok, &p->pinned[0], 4, hipMemcpyHostToDevice, p->stream));
+        QH_TRY(hipMemcpyAsync(p->pos, &p->pinned[1], 4, hipMemcpyHostToDevice, p->stream));
+        QH_TRY(hipGraphLaunch(p->step_graph, p->stream));
+    }
+    QH_TRY(hipMemcpyAsync(logits, p->logits, (size_t)model->config.vocab_size * 4, hipMemcpyDeviceToHost,
+                          p->stream));
+    QH_TRY(hipStreamSynchronize(p->stream));
+    return Q_OK;
+}
+
+// Reference src/main.c:852-881, greedy branch, argmax on the GPU.
+q_error_code q_sample_token(const float* __restrict__ logits, uint32_t vocab_size, float temperature,
+                            uint32_t top_k, float top_p, uint32_t* __restrict__ token_id_out,
+                            q_context* __restrict__ ctx) {
+    (void)top_k;
+    (void)top_p;
+    (void)ctx;
+    if (!logits || !token_id_out) return Q_ERR_INVALID_ARG;
+    if (vocab_size == 0) return Q_ERR_INVALID_SIZE;
+    if (!(temperature >= 0.0f) || !std::isfinite(temperature)) return Q_ERR_INVALID_ARG;
+    if (!(temperature < 1e-6f)) return Q_ERR_INVALID_ARG;  // sampling is not part of this build
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    void* buf;
+    QH_TRY_CODE(stage(d, 1, (size_t)vocab_size * 4 + 256, &buf));
+    float* dl = static_cast<float*>(buf);
+    uint32_t* di = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(buf) + (((size_t)vocab_size * 4 + 255) & ~(size_t)255));
+    QH_TRY(hipMemcpyAsync(dl, logits, (size_t)vocab_size * 4, hipMemcpyHostToDevice, d->stream));
+    QH_TRY(launch_argmax(dl, vocab_size, di, d->stream));
+    QH_TRY(hipMemcpyAsync(token_id_out, di, 4, hipMemcpyDeviceToHost, d->stream));
+    QH_TRY(hipStreamSynchronize(d->stream));
+    return Q_OK;
+}
+
+// Greedy generation on the device: n_steps decode steps from (token, pos),
+// each step's argmax fed back as the next token and the position advanced
+// on the device (no host round trip between steps).  tokens_out (host,
+// n_steps entries) receives the generated tokens; *ms_per_step the mean
+// step time measured with HIP events over the n_steps graph replays.
+q_error_code qh_llama_generate(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
+                               uint32_t n_steps, uint32_t* tokens_out, float* ms_per_step) {
+    if (!model || !ctx || !tokens_out) return Q_ERR_INVALID_ARG;
+    if (n_steps == 0) return Q_ERR_INVALID_SIZE;
+    if (token >= model->config.vocab_size) return Q_ERR_INVALID_ARG;
+    if ((uint64_t)pos + n_steps > model->config.max_seq_len) return Q_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    ModelPlan* p = plan_of(model, ctx);
+    if (!p) return Q_ERR_INVALID_ARG;
+    QH_TRY_CODE(check_kv(p, ctx));
+    QH_TRY_CODE(bind_kv(p, ctx));
+    if (!p->gen_graph) QH_TRY_CODE(capture(p, true, &p->gen_graph));
+    QH_TRY(hipStreamSynchronize(p->stream));
+    p->pinned[0] = token;
+    p->pinned[1] = pos;
+    p->pinned[2] = 0;
+    QH_TRY(hipMemcpyAsync(p->tok, &p->pinned[0], 4, hipMemcpyHostToDevice, p->stream));
+    QH_TRY(hipMemcpyAsync(p->pos, &p->pinned[1], 4, hipMemcpyHostToDevice, p->stream));
+    QH_TRY(hipMemcpyAsync(p->hist_n, &p->pinned[2], 4, hipMemcpyHostToDevice, p->stream));
+    hipEvent_t e0, e1;
+    QH_TRY(hipEventCreate(&e0));
+    QH_TRY(hipEventCreate(&e1));
+    QH_TRY(hipEventRecord(e0, p->stream));
+    for (uint32_t i = 0; i < n_steps; ++i) QH_TRY(hipGraphLaunch(p->gen_graph, p->stream));
+    QH_TRY(hipEventRecord(e1, p->stream));
+    QH_TRY(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    QH_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (ms_per_step) *ms_per_step = ms / (float)n_steps;
+    QH_TRY(hipMemcpy(tokens_out, p->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
+    return Q_OK;
+}
+
+}  // extern "C"

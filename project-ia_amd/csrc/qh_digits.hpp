@@ -1,0 +1,68 @@
+// qh_digits.hpp -- device code that turns fp32 activations into the signed
+// 4-bit digit planes consumed by the Q4_0 GEMV (k_q4.hip).  Any kernel that
+// produces a GEMV input can emit its digits directly with prep_lane().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+namespace qh {
+
+// Per 32-element block of x: k with |round(x * 2^k)| <= kDigitMax (23-24
+// significant bits for the block maximum), the 6 balanced base-16 digits of
+// x_int = round(x * 2^k) stored as 6 planes of 8 signed nibbles per dword
+// (plane p, dword i holds elements 8i..8i+7), and a word z = 0 (or NaN when
+// the block holds a NaN or infinity, which makes every dot product with the
+// block NaN).  Layout: uint4 xd[7][pad]; planes 0..5, then (k, z, 0, 0).
+//
+// prep_lane: 32 consecutive lanes own one block (lane = element); block max
+// and NaN/Inf flag by cross-lane reductions, then the digits and the 8-lane
+// OR that packs each plane dword.  Lanes 0..5 of each 8-lane group store
+// plane dwords, lanes 6..7 of the first group store (k, z).  Every lane of
+// the wave must call it (it uses cross-lane operations).
+constexpr int kDigitMax = 7829367;         // 7 * (16^6 - 1) / 15: largest 6-digit balanced value
+constexpr uint32_t kDigitBias = 8947848u;  // 8 * (16^6 - 1) / 15
+
+__device__ inline void prep_lane(float v, uint32_t c, bool store, uint32_t pad, uint32_t* __restrict__ xd) {
+    const int e = threadIdx.x & 31;
+    const float a = fabsf(v);
+    const bool bad_here = !(a <= FLT_MAX);  // NaN or infinity
+    float m = bad_here ? 0.0f : a;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    const uint64_t bm = __ballot(bad_here);
+    const uint32_t grp = (threadIdx.x & 32) ? (uint32_t)(bm >> 32) : (uint32_t)bm;
+    const bool bad = grp != 0u;
+    int k = 0;
+    if (!bad && m > 0.0f) {
+        const int E = __builtin_amdgcn_frexp_expf(m);  // m < 2^E
+        k = 23 - E;
+        if (rintf(ldexpf(m, k)) > (float)kDigitMax) k -= 1;
+    }
+    const int xi = bad ? 0 : (int)rintf(ldexpf(v, k));
+    const uint32_t u = (uint32_t)(xi + (int)kDigitBias);  // 6 unsigned nibbles = digit + 8
+    const int sh = 4 * (e & 7);
+    uint32_t pl[6];
+#pragma unroll
+    for (int p = 0; p < 6; ++p) pl[p] = ((u >> (4 * p)) & 15u) << sh;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1)
+#pragma unroll
+        for (int p = 0; p < 6; ++p) pl[p] |= __shfl_xor(pl[p], off, 8);
+    if (!store) return;
+    const int q = e & 7, i = e >> 3;
+    if (q < 6) {
+        uint32_t val = pl[0];
+#pragma unroll
+        for (int p = 1; p < 6; ++p) val = (q == p) ? pl[p] : val;
+        xd[((size_t)q * pad + c) * 4 + i] = val ^ 0x88888888u;
+    } else if (i == 0) {
+        const float z = bad ? __builtin_nanf("") : 0.0f;
+        xd[((size_t)6 * pad + c) * 4 + (q - 6)] = (q == 6) ? (uint32_t)k : __float_as_uint(z);
+    }
+}
+
+
+}  // namespace qh

@@ -34,11 +34,26 @@ struct GemvSeg {
     float* y;             // output [M]
     const float* res;     // optional residual [M] (y = res + W.x)
     uint32_t M;
+    // Decode-step epilogue (hd == 0: plain contiguous store).  With hd > 0
+    // output row r is stored at y + pos*pos_stride + (r/hd)*head_stride +
+    // r%hd, pos read from GemvDecode::pos; with rope the pair (r&~1, r|1) is
+    // first rotated by the tables at row pos (reference src/ops/avx2/rope.c).
+    uint32_t hd = 0;
+    uint32_t head_stride = 0;
+    uint32_t pos_stride = 0;
+    bool rope = false;
+};
+
+// Device-side state read by decode-step epilogues.
+struct GemvDecode {
+    const uint32_t* pos = nullptr;  // current position (device)
+    const float* cos_tab = nullptr; // [max_seq][hd] duplicated-pair tables
+    const float* sin_tab = nullptr;
 };
 
 // y = W . x for up to 4 segments sharing the same x (digit planes xd).
 hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd,
-                       hipStream_t s);
+                       hipStream_t s, const GemvDecode* dec = nullptr);
 
 // ---- vector kernels (k_vec.hip) ----
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s);
