@@ -68,9 +68,9 @@ class LayerSet:
 
 
 def gen_layer(seed):
-    from oracle import oracle as orc
-    rng = orc.rng_for(seed)
-    return {k: orc.gen_q4(M, N, rng) for k, M, N in SHAPES}
+    from qorus_amd import synthetic as syn
+    rng = syn.rng_for(seed)
+    return {k: syn.gen_q4(M, N, rng) for k, M, N in SHAPES}
 
 
 def ptr_array(ptrs, ctype=C.c_void_p):
@@ -79,15 +79,15 @@ def ptr_array(ptrs, ctype=C.c_void_p):
 
 def run_gpu(args):
     import qorus_amd as qa
-    from oracle import oracle as orc
+    from qorus_amd import synthetic as syn
     lib = qa.lib()
     if not qa.gpu_available():
         raise SystemExit("bench.py: no usable GPU (" + lib.qh_last_error().decode() + ")")
     log(f"[bench] device {lib.qh_arch_name().decode()}; generating {LAYERS} layers "
         f"({LAYERS * STEP_BYTES / 1e6:.0f} MB)")
     layers = [LayerSet(qa, gen_layer(1000 + l)) for l in range(LAYERS)]
-    rng = orc.rng_for(77)
-    xin = {k: qa.DeviceBuffer.from_numpy(orc.gen_f32(n, rng)) for k, n in
+    rng = syn.rng_for(77)
+    xin = {k: qa.DeviceBuffer.from_numpy(syn.gen_f32(n, rng)) for k, n in
            (("h", DIM), ("o", DIM), ("h2", DIM), ("m", HID))}
     outs = {k: qa.DeviceBuffer(M * 4) for k, M, _ in SHAPES}
     ws = {k: qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(n)) for k, n in
@@ -220,6 +220,111 @@ def run_cpu_baseline(seconds):
                       f"in {el:.1f} s on 1 pinned core ({orc.cpu_model_name()})"}
 
 
+# ---------------------------------------------------------------------------
+# Decode step
+# ---------------------------------------------------------------------------
+DEC = dict(vocab=128256, dim=4096, hidden=14336, n_layers=32, n_heads=32, n_kv=8)
+DEC_POS = 2047
+
+
+def decode_bytes_per_token(n_layers=32, ctx=2048):
+    """Algorithmic HBM bytes of one decode step: every weight byte once
+    (32 layers + Q4_0 LM head + the fp32 embedding row and norm weights) and
+    the fp32 K and V rows of `ctx` cached positions."""
+    d, hid, v, kvd = 4096, 14336, 128256, 1024
+    q4 = lambda r, c: r * (c // 32) * 20
+    layer = q4(d, d) * 2 + q4(kvd, d) * 2 + q4(hid, d) * 2 + q4(d, hid) + 2 * d * 4
+    kv = n_layers * 8 * ctx * 2 * 128 * 4
+    return n_layers * layer + q4(v, d) + d * 4 + d * 4 + kv
+
+
+def scratch_dir(need_bytes):
+    import shutil
+    import tempfile
+    for base in ("/dev/shm", None):
+        try:
+            d = tempfile.mkdtemp(prefix="qorus_bench_", dir=base)
+            if shutil.disk_usage(d).free > need_bytes * 1.2:
+                return d
+            shutil.rmtree(d, ignore_errors=True)
+        except OSError:
+            continue
+    raise SystemExit("bench.py: no scratch space for the synthetic model")
+
+
+def run_decode(args):
+    import shutil
+    import qorus_amd as qa
+    from qorus_amd import synthetic as syn
+    steps = args.decode_steps
+    max_seq = DEC_POS + 1 + args.decode_warmup + steps + 8
+    h = qa.QorusHeader(max_seq=max_seq, **DEC)
+    size = qa.model_layout(h)["_size"]
+    d = scratch_dir(size)
+    path = Path(d) / "llama3_8b_q4_0.qorus"
+    try:
+        t0 = time.perf_counter()
+        syn.write_synthetic_model(path, h, seed=2024)
+        log(f"[bench] decode: wrote {size / 1e9:.2f} GB synthetic model in {time.perf_counter() - t0:.1f} s")
+        m = qa.Model(path)
+        hd = 128
+        rng = syn.rng_for(2025)
+        kv = np.zeros((h.n_layers, h.n_kv, max_seq, 2, hd), np.float32)
+        kv[:, :, :DEC_POS] = rng.standard_normal((h.n_layers, h.n_kv, DEC_POS, 2, hd), dtype=np.float32)
+        m.upload_kv(kv)
+        first_tok = 1
+        # warm-up (captures the graph), then the timed greedy decode from pos 2047
+        m.generate(first_tok, DEC_POS, args.decode_warmup)
+        m.upload_kv(kv)
+        toks, ms = m.generate(first_tok, DEC_POS, steps)
+        m.close()
+        avg_ctx = DEC_POS + 1 + (steps - 1) / 2
+        bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
+        out = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "steps": steps,
+               "warmup": args.decode_warmup,
+               "workload": "config4: 32-layer Llama-3-8B shape, Q4_0 weights + Q4_0 LM head, fp32 KV pre-filled "
+                           "N(0,1) to pos 2047, greedy decode from pos 2047 (context 2048..%d), hipGraph per step"
+                           % (DEC_POS + steps),
+               "hbm_bytes_per_token": bpt,
+               "achieved_GB_s": round(bpt / (ms * 1e-3) / 1e9, 1),
+               "frac_of_hbm_peak": round(bpt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1)}
+        if not args.no_cpu:
+            out["cpu_baseline"], out["first_token_matches_cpu"] = run_cpu_decode(path, kv, first_tok, int(toks[0]),
+                                                                                args.cpu_decode_tokens)
+        return out
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def run_cpu_decode(path, kv, first_tok, gpu_tok0, n_tokens):
+    """The oracle's corrected decode step (or_decode_step), one pinned core."""
+    from oracle import oracle as orc
+    blob = np.memmap(path, dtype=np.uint8, mode="r")
+    ref = orc.DecodeOracle(blob, kv.copy())
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        t = first_tok
+        t0 = time.perf_counter()
+        toks = []
+        for i in range(n_tokens):
+            t, _ = ref.step(t, DEC_POS + i)
+            toks.append(t)
+        el = time.perf_counter() - t0
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    cpu = {"value": round(n_tokens / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"{n_tokens} greedy decode steps of the 32-layer model from pos 2047 with the oracle's "
+                     f"C restatement (or_decode_step; the reference's own forward cannot run at these shapes) "
+                     f"in {el:.1f} s on 1 pinned core ({orc.cpu_model_name()})"}
+    return cpu, bool(toks[0] == gpu_tok0)
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (profiles/gemv_gate_up_traffic.json), or None."""
@@ -236,7 +341,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
+    ap.add_argument("--decode-steps", type=int, default=32)
+    ap.add_argument("--decode-warmup", type=int, default=4)
+    ap.add_argument("--cpu-decode-tokens", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (batch-1 decode of an 8B model is not "
@@ -247,6 +356,7 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = STEP_BYTES * args.steps / wall / 1e9
     cpu = None if args.no_cpu else run_cpu_baseline(args.cpu_seconds)
+    decode = None if args.no_decode else run_decode(args)
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -271,6 +381,7 @@ def main():
                      "alg_bytes_per_launch": GATE_UP_BYTES, "mean_launch_us": round(kern_ms * 1e3, 2)},
         "kernels": breakdown,
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     print(json.dumps(out), flush=True)
 

@@ -63,20 +63,25 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) mx[h] = -INFINITY;
     const float* kbase = kv + (size_t)kvh * head_stride;
-    // 64 keys per workgroup: each wave takes 16, two per step (one per half).
-#pragma unroll 1
+    // 64 keys per workgroup: each wave takes 16, two per step (one per half);
+    // all 8 steps' key values are loaded before any is used.
+    float kk[8][4];
+#pragma unroll
+    for (int step = 0; step < 8; ++step) {
+        const uint32_t j = j0 + (uint32_t)(wave * 16 + step * 2 + half);
+        const float* krow = kbase + (size_t)(j < S ? j : 0u) * (2 * kHd);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kk[step][t] = krow[32 * t + 8 * c + l];
+    }
+#pragma unroll
     for (int step = 0; step < 8; ++step) {
         const uint32_t j = j0 + (uint32_t)(wave * 16 + step * 2 + half);
         const bool valid = j < S;
-        const float* krow = kbase + (size_t)(valid ? j : 0u) * (2 * kHd);
-        float kk[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) kk[t] = krow[32 * t + 8 * c + l];
 #pragma unroll
         for (uint32_t h = 0; h < group; ++h) {
             float acc = 0.0f;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc = fmaf(qv[h][t], kk[t], acc);
+            for (int t = 0; t < 4; ++t) acc = fmaf(qv[h][t], kk[step][t], acc);
             const float d = dot_tree32(acc);
             const float sc = d * scale;
             if (valid && (lane & 31) == 0) scores[(size_t)(kvh * group + h) * max_seq + j] = sc;
@@ -113,11 +118,18 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
     __shared__ float o_s[kMaxGroup][kHd];
     __shared__ float gmax[kMaxGroup];
     const uint32_t tid = threadIdx.x;
-    if (tid < group) {
-        const uint32_t h = kvh * group + tid;
-        float m = -INFINITY;
-        for (uint32_t c = 0; c < nch; ++c) m = fmaxf(m, part_max[(size_t)h * n_chunks + c]);
-        gmax[tid] = m;
+    // Global max per head: one wave per head (lane-strided loads, then a
+    // butterfly max); exact, so the order does not matter.
+    {
+        const uint32_t wv = tid >> 6, ln = tid & 63;
+        for (uint32_t hh = wv; hh < group; hh += 4) {
+            const uint32_t h = kvh * group + hh;
+            float m = -INFINITY;
+            for (uint32_t c = ln; c < nch; c += 64) m = fmaxf(m, part_max[(size_t)h * n_chunks + c]);
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            if (ln == 0) gmax[hh] = m;
+        }
     }
     __syncthreads();
     // e_j for the chunk's keys and all group heads.
@@ -174,7 +186,21 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     if (valid) {
         const uint32_t h = t / kHd;
         float total = 0.0f, acc = 0.0f;
-        for (uint32_t c = 0; c < nch; ++c) {
+        uint32_t c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            float ps[8], op[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ps[u] = part_sum[(size_t)h * n_chunks + c + u];
+                op[u] = o_part[(size_t)(c + u) * N + t];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                total += ps[u];
+                acc += op[u];
+            }
+        }
+        for (; c < nch; ++c) {
             total += part_sum[(size_t)h * n_chunks + c];
             acc += o_part[(size_t)c * N + t];
         }

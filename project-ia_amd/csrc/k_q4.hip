@@ -152,6 +152,246 @@ struct GemvArgs {
     const float* sin_tab;
 };
 
+// Integer dots of R*J blocks (already loaded) against the x digit planes,
+// accumulated into acc[0..R): plane by plane across all blocks, each plane a
+// 4-deep dot8 chain of its own, planes combined by P = (P << 4) + S_p, so
+// the independent chains of different blocks interleave; then
+// acc += ldexp(fma(s, (float)P, z), -k) per block.
+template <int R, int J>
+__device__ __forceinline__ void dot_batch(const uint4 (&q)[R][J], const float (&s)[R][J], const uint4 (&xp)[J][6],
+                                          const int (&kk)[J], const float (&zz)[J], const bool (&ok)[J],
+                                          float (&acc)[R]) {
+    int P[R][J];
+    uint32_t wq[R][J][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            wq[r][j][0] = q[r][j].x ^ 0x88888888u;
+            wq[r][j][1] = q[r][j].y ^ 0x88888888u;
+            wq[r][j][2] = q[r][j].z ^ 0x88888888u;
+            wq[r][j][3] = q[r][j].w ^ 0x88888888u;
+            P[r][j] = 0;
+        }
+#pragma unroll
+    for (int p = 5; p >= 0; --p)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                int sp = __builtin_amdgcn_sdot8((int)wq[r][j][0], (int)xp[j][p].x, 0, false);
+                sp = __builtin_amdgcn_sdot8((int)wq[r][j][1], (int)xp[j][p].y, sp, false);
+                sp = __builtin_amdgcn_sdot8((int)wq[r][j][2], (int)xp[j][p].z, sp, false);
+                sp = __builtin_amdgcn_sdot8((int)wq[r][j][3], (int)xp[j][p].w, sp, false);
+                P[r][j] = (int)((uint32_t)P[r][j] << 4) + sp;
+            }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const float sc = ok[j] ? s[r][j] : 0.0f;
+            const float c = fmaf(sc, (float)P[r][j], zz[j]);
+            acc[r] += ldexpf(c, -kk[j]);
+        }
+}
+
+// Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
+__device__ __forceinline__ void seg_of(const GemvArgs& a, uint32_t t, uint32_t& sg, uint32_t& tbase) {
+    sg = 0;
+    tbase = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (sg + 1 < a.nseg && t >= a.tile_end[sg]) {
+            tbase = a.tile_end[sg];
+            ++sg;
+        }
+    }
+}
+
+// Raw buffer resource word 3 for gfx9-family parts (32-bit untyped data, no
+// swizzle); out-of-range reads return zero.
+constexpr int kBufFlags = 0x00020000;
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+
+// Store one finished row (value v, RoPE partner pv) of segment sg, with the
+// residual rv and the RoPE cos/sin (c, sn) of the row already loaded.  RoPE
+// pairs (x0, x1) = (row&~1, row|1): y0 = x0*c - x1*s, y1 = x1*c + x0*s,
+// products rounded separately.
+__device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, uint32_t row, float v, float pv,
+                                              bool odd, uint32_t pos, float rv, float c, float sn) {
+    const uint32_t M = a.M[sg];
+    if (row >= M) return;
+    float* __restrict__ y = a.y[sg];
+    const uint32_t hd = a.hd[sg];
+    float* dst = y + row;
+    if (hd) {
+        const uint32_t i = row % hd;
+        if ((a.rope_mask >> sg) & 1u) {
+            const float t0 = v * c, t1 = pv * sn;
+            v = odd ? t0 + t1 : t0 - t1;
+        }
+        dst = y + (size_t)pos * a.pos_stride[sg] + (size_t)(row / hd) * a.head_stride[sg] + i;
+    }
+    *dst = a.res[sg] ? rv + v : v;
+}
+
+// ---------------------------------------------------------------------------
+// Persistent GEMV (input fits one K-chunk: nblk <= 64*W*J).  A "wave group"
+// of W waves covers all K columns; it loads its x digits once, then walks
+// row tiles of RT rows (tile u, u + stride, ...), loading the next tile's
+// blocks while it computes the current one.  A workgroup holds G wave
+// groups (G > 1 only with W == 1: the cross-wave reduction of W > 1 needs
+// the whole workgroup on one tile).  The grid is sized to what stays
+// resident, so there is one wave of workgroups and no per-tile prologue.
+// ---------------------------------------------------------------------------
+template <int W, int J, int G, int RT>
+__global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
+    static_assert(W == 1 || G == 1, "multi-wave K split runs one tile per workgroup");
+    const int lane = threadIdx.x & 63;
+    // The wave index is uniform per wave; readfirstlane makes that visible to
+    // the compiler so tile/segment bookkeeping stays scalar (a vector load of
+    // a kernel argument would add vmcnt waits that drain the prefetch).
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int kw = wave % W;
+    const int g = wave / W;
+    const uint32_t row_bytes = a.nblk * 20u;
+    const uint32_t total = a.tile_end[a.nseg - 1];
+    const uint32_t stride = gridDim.x * G;
+    const uint32_t pos = a.pos ? __builtin_amdgcn_readfirstlane(*a.pos) : 0u;
+
+    uint32_t coff[J];
+    bool ok[J];
+    uint4 xp[J][6];
+    int kk[J];
+    float zz[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
+        ok[j] = col < a.nblk;
+        const uint32_t cc = ok[j] ? col : 0u;
+        coff[j] = cc * 20u;
+#pragma unroll
+        for (int p = 0; p < 6; ++p) {
+            const uint4 v = a.xd[(size_t)p * a.pad + cc];
+            xp[j][p] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+        const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
+        kk[j] = ok[j] ? (int)meta.x : 0;
+        zz[j] = ok[j] ? __uint_as_float(meta.y) : 0.0f;
+    }
+
+    // Row r of a tile is read through a buffer resource whose base is the
+    // row and whose size is the row's bytes (0 past the last row): the
+    // per-lane column offsets stay fixed for the whole kernel, the row base
+    // lives in scalar registers, and out-of-range rows, columns and tiles
+    // read zeros (a zero scale) without touching memory.  Every load is
+    // therefore unconditional, and the epilogue's operands (residual,
+    // RoPE cos/sin of the row a lane stores) are loaded with the tile: an
+    // epilogue load, or a prefetch under a branch, would make the in-order
+    // vmcnt wait drain the next tile's loads.
+    struct Epi {
+        float res, c, sn;
+    };
+    auto load_tile = [&](uint32_t u, uint4 (&q)[RT][J], float (&s)[RT][J], Epi& e) {
+        uint32_t sg, tbase;
+        seg_of(a, u, sg, tbase);
+        const uint8_t* __restrict__ wseg = a.w[sg];
+        const uint32_t M = a.M[sg];
+        const uint32_t row0 = (u - tbase) * RT;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t row = row0 + (uint32_t)r;
+            const int nrec = row < M ? (int)row_bytes : 0;
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(wseg + (size_t)row * row_bytes), 0, nrec, kBufFlags);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(rs, coff[j], 0, 0);
+                q[r][j] = make_uint4(v[0], v[1], v[2], v[3]);
+                s[r][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, coff[j] + 16u, 0, 0));
+            }
+        }
+        const uint32_t erow = row0 + (uint32_t)(lane & (RT - 1));
+        const float* res = a.res[sg];
+        const __amdgpu_buffer_rsrc_t rr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)res, 0, res ? (int)(M * 4u) : 0, kBufFlags);
+        e.res = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, erow * 4u, 0, 0));
+        const uint32_t hd = a.hd[sg];
+        const bool rope = (a.rope_mask >> sg) & 1u;
+        const uint32_t hdr = rope ? hd : 0u;
+        const uint32_t i = rope ? erow % hd : 0u;
+        const __amdgpu_buffer_rsrc_t rc =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.cos_tab + (size_t)pos * hdr), 0, (int)(hdr * 4u), kBufFlags);
+        const __amdgpu_buffer_rsrc_t rn =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.sin_tab + (size_t)pos * hdr), 0, (int)(hdr * 4u), kBufFlags);
+        e.c = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, i * 4u, 0, 0));
+        e.sn = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rn, i * 4u, 0, 0));
+    };
+
+    auto finish_tile = [&](uint32_t u, const uint4 (&q)[RT][J], const float (&s)[RT][J], const Epi& e) {
+        float acc[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r] = 0.0f;
+        dot_batch<RT, J>(q, s, xp, kk, zz, ok, acc);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            float v = acc[r];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            acc[r] = v;
+        }
+        uint32_t sg, tbase;
+        seg_of(a, u, sg, tbase);
+        const uint32_t row0 = (u - tbase) * RT;
+        if constexpr (W == 1) {
+            if (lane < RT) {
+                float v = acc[0], pv = acc[1];
+#pragma unroll
+                for (int r = 1; r < RT; ++r) v = (r == lane) ? acc[r] : v;
+#pragma unroll
+                for (int r = 0; r < RT; ++r) pv = (r == (lane ^ 1)) ? acc[r] : pv;
+                store_row_pre(a, sg, row0 + lane, v, pv, lane & 1, pos, e.res, e.c, e.sn);
+            }
+        } else {
+            __shared__ float red[W][RT];
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < RT; ++r) red[kw][r] = acc[r];
+            }
+            __syncthreads();
+            if ((int)threadIdx.x < RT) {
+                const int r = threadIdx.x;
+                float v = red[0][r];
+#pragma unroll
+                for (int k2 = 1; k2 < W; ++k2) v += red[k2][r];
+                store_row_pre(a, sg, row0 + r, v, 0.0f, false, pos, e.res, e.c, e.sn);
+            }
+            __syncthreads();  // red[] is reused by the next tile
+        }
+    };
+
+    uint4 qa[RT][J], qb[RT][J];
+    float sa[RT][J], sb[RT][J];
+    Epi ea, eb;
+    uint32_t u = blockIdx.x * G + g;
+    load_tile(u, qa, sa, ea);
+    // The scheduling barriers keep the next tile's loads issued before any
+    // instruction that waits on the current tile's data.
+    while (u < total) {
+        uint32_t un = u + stride;
+        load_tile(un, qb, sb, eb);
+        __builtin_amdgcn_sched_barrier(0);
+        finish_tile(u, qa, sa, ea);
+        u = un;
+        if (u >= total) break;
+        un = u + stride;
+        load_tile(un, qa, sa, ea);
+        __builtin_amdgcn_sched_barrier(0);
+        finish_tile(u, qb, sb, eb);
+        u = un;
+    }
+}
+
 // W waves split K, G independent row groups per workgroup, RW rows per wave
 // (processed R at a time, the next batch loaded while the current one is
 // computed), J block columns per lane per K-chunk (K-chunk = 64*W*J blocks).
@@ -178,7 +418,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
     const uint32_t M = a.M[sg];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int kw = wave % W;
     const int g = wave / W;
     const uint32_t row0 = (t - tbase) * (G * RW) + g * RW;
@@ -366,21 +606,74 @@ static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const u
     return hipGetLastError();
 }
 
-// Launch shape by input width (nblk = N/32 blocks) and total rows.
+static int g_num_cu = 0;
+
+static int num_cu() {
+    if (g_num_cu == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_num_cu = n;
+        else
+            g_num_cu = 256;
+    }
+    return g_num_cu;
+}
+
+template <int W, int J, int G, int RT>
+static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
+                             const GemvDecode* dec) {
+    GemvArgs a{};
+    uint32_t tiles = 0;
+    for (int i = 0; i < 4; ++i) {
+        if (i < nseg) {
+            a.w[i] = segs[i].w;
+            a.y[i] = segs[i].y;
+            a.res[i] = segs[i].res;
+            a.M[i] = segs[i].M;
+            a.hd[i] = segs[i].hd;
+            a.head_stride[i] = segs[i].head_stride;
+            a.pos_stride[i] = segs[i].pos_stride;
+            if (segs[i].rope) a.rope_mask |= 1u << i;
+            if (segs[i].hd && (W != 1 || !dec || !dec->pos || (segs[i].hd % 2) != 0)) return hipErrorInvalidValue;
+            if (segs[i].rope && (!dec->cos_tab || !dec->sin_tab || (RT % 2) != 0)) return hipErrorInvalidValue;
+            tiles += (segs[i].M + RT - 1) / RT;
+        }
+        a.tile_end[i] = tiles;
+    }
+    a.nseg = (uint32_t)nseg;
+    a.nblk = nblk;
+    a.pad = xd_pad(nblk);
+    a.xd = xd;
+    if (dec) {
+        a.pos = dec->pos;
+        a.cos_tab = dec->cos_tab;
+        a.sin_tab = dec->sin_tab;
+    }
+    if (tiles == 0) return hipSuccess;
+    static int occ = 0;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT>, 64 * W * G, 0) != hipSuccess || o < 1)
+            o = 1;
+        occ = o;
+    }
+    const uint32_t groups = (tiles + G - 1) / G;
+    const uint32_t resident = (uint32_t)(occ * num_cu());
+    const uint32_t grid = groups < resident ? groups : resident;
+    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT>), dim3(grid), dim3(64 * W * G), 0, s, a);
+    return hipGetLastError();
+}
+
+// Launch shape by input width (nblk = N/32 blocks).  Inputs that fit one
+// K-chunk use the persistent kernel; wider ones the tile-per-workgroup one.
 hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
                        const GemvDecode* dec) {
     if (nseg < 1 || nseg > 4) return hipErrorInvalidValue;
-    uint64_t rows = 0;
-    for (int i = 0; i < nseg; ++i) rows += segs[i].M;
-    const bool many_rows = rows >= 16384;
-    if (nblk <= 64) return run_gemv<1, 1, 4, 4, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 128) {
-        if (many_rows) return run_gemv<1, 2, 4, 8, 4>(segs, nseg, nblk, xd, s, dec);
-        return run_gemv<1, 2, 4, 4, 4>(segs, nseg, nblk, xd, s, dec);
-    }
-    if (nblk <= 256) return run_gemv<2, 2, 2, 8, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 448) return run_gemv<7, 1, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 512) return run_gemv<8, 1, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, xd, s, dec);
     return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
 }
 

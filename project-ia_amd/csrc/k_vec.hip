@@ -171,7 +171,20 @@ __global__ __launch_bounds__(kVecThreads) void k_argmax(const float* __restrict_
     __shared__ uint32_t si[kVecThreads / 64];
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < N; i += kVecThreads) {
+    // 8 loads in flight per thread per round.
+    uint32_t i = threadIdx.x;
+    for (; i + 7 * kVecThreads < N; i += 8 * kVecThreads) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = x[i + u * kVecThreads];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (arg_better(v[u], i + u * kVecThreads, bv, bi)) {
+                bv = v[u];
+                bi = i + u * kVecThreads;
+            }
+    }
+    for (; i < N; i += kVecThreads) {
         const float v = x[i];
         if (arg_better(v, i, bv, bi)) {
             bv = v;

@@ -66,17 +66,38 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return s;
 }
 
-// RMSNorm scale r for x[0..N) (fixed-order tree sum of squares; mean =
-// sum/(float)N; a = mean + eps; r0 = rsq(a); one Newton step
-// (r0*(3 - a*(r0*r0)))*0.5 as in reference src/ops/avx2/rmsnorm.c:62-71).
+// RMSNorm scale r for x[0..N), N % 4 == 0 (fixed-order tree sum of squares:
+// each thread accumulates its float4s (4 lane partials), then the lanes of
+// the float4, then block_sum; mean = sum/(float)N; a = mean + eps;
+// r0 = rsq(a); one Newton step (r0*(3 - a*(r0*r0)))*0.5 as in reference
+// src/ops/avx2/rmsnorm.c:62-71).  Loads are issued 4 at a time so a thread
+// keeps several in flight.
 template <int NT>
 __device__ __forceinline__ float rms_scale(const float* __restrict__ x, uint32_t N, float eps, float* red) {
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < N; i += NT) {
-        const float v = x[i];
-        const float sq = v * v;
-        ss = ss + sq;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const uint32_t n4 = N / 4;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    uint32_t i = threadIdx.x;
+    for (; i + 3 * NT < n4; i += 4 * NT) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = x4[i + u * NT];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            s0 = s0 + v[u].x * v[u].x;
+            s1 = s1 + v[u].y * v[u].y;
+            s2 = s2 + v[u].z * v[u].z;
+            s3 = s3 + v[u].w * v[u].w;
+        }
     }
+    for (; i < n4; i += NT) {
+        const float4 v = x4[i];
+        s0 = s0 + v.x * v.x;
+        s1 = s1 + v.y * v.y;
+        s2 = s2 + v.z * v.z;
+        s3 = s3 + v.w * v.w;
+    }
+    const float ss = (s0 + s1) + (s2 + s3);
     const float sum = block_sum<NT>(ss, red);
     const float mean = sum / (float)N;
     const float a = mean + eps;
