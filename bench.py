@@ -325,6 +325,83 @@ def run_cpu_decode(path, kv, first_tok, gpu_tok0, n_tokens):
     return cpu, bool(toks[0] == gpu_tok0)
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic of the dominant kernel (rocprofv3 --pmc passes)
+# ---------------------------------------------------------------------------
+COPY_BYTES = 256 << 20
+TRAFFIC_LAUNCHES = 24
+
+
+def run_traffic():
+    """Workload of the counter passes: TRAFFIC_LAUNCHES fused W_gate|W_up
+    GEMV launches (rotating LAYERS distinct weight sets) and 4 device copies
+    of COPY_BYTES, whose counter readings calibrate the KiB-per-dispatch
+    scale.  Run it under `rocprofv3 --pmc FETCH_SIZE` and, separately,
+    `--pmc WRITE_SIZE`; then --summarize-traffic."""
+    import qorus_amd as qa
+    from qorus_amd import synthetic as syn
+    lib = qa.lib()
+    if not qa.gpu_available():
+        raise SystemExit("bench.py: no usable GPU")
+    layers = [LayerSet(qa, gen_layer(1000 + l)) for l in range(LAYERS)]
+    x = qa.DeviceBuffer.from_numpy(syn.gen_f32(DIM, syn.rng_for(77)))
+    ws = qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(DIM))
+    outs = [qa.DeviceBuffer(HID * 4) for _ in range(2)]
+    src, dst = qa.DeviceBuffer(COPY_BYTES), qa.DeviceBuffer(COPY_BYTES)
+    stream = qa.Stream()
+    s = stream.handle
+    qa.check(lib.qh_gemv_prepare(x.ptr, DIM, ws.ptr, s))
+    ys = ptr_array([o.ptr for o in outs])
+    for i in range(TRAFFIC_LAUNCHES):
+        L = layers[i % LAYERS]
+        Ws = ptr_array([L.t["w_gate"].addr, L.t["w_up"].addr])
+        qa.check(lib.qh_gemv_q4_f32_prepared(Ws, None, ys, 2, ws.ptr, s))
+    stream.sync()
+    for _ in range(4):
+        qa.check(lib.qh_memcpy_dtod(dst.ptr, src.ptr, COPY_BYTES, s))
+    stream.sync()
+    print(json.dumps({"traffic_workload": "gate_up", "launches": TRAFFIC_LAUNCHES, "copy_bytes": COPY_BYTES}))
+
+
+def _counter_rows(d):
+    import csv
+    rows = []
+    for f in Path(d).rglob("*counter_collection.csv"):
+        rows += list(csv.DictReader(open(f)))
+    if not rows:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    return rows
+
+
+def summarize_traffic(fetch_dir, write_dir, cmd):
+    """profiles/gemv_gate_up_traffic.json from the two counter passes.
+    Each counter's KiB-per-dispatch reading is scaled by copy_bytes / (what
+    the same counter reads for the device copy), so the figure is in bytes
+    of the copy's own accounting."""
+    out = {}
+    for name, d, copy_side in (("FETCH_SIZE", fetch_dir, "read"), ("WRITE_SIZE", write_dir, "write")):
+        rows = [r for r in _counter_rows(d) if r.get("Counter_Name") == name]
+        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv" in r["Kernel_Name"]]
+        copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        gmax = max((int(r["Grid_Size"]) for r in copies), default=0)
+        copy = [float(r["Counter_Value"]) for r in copies if int(r["Grid_Size"]) == gmax]
+        if not gemv or not copy:
+            raise SystemExit(f"{name}: no gemv ({len(gemv)}) or copy ({len(copy)}) dispatches")
+        g = float(np.median(gemv[2:] if len(gemv) > 4 else gemv))
+        c = float(np.median(copy))
+        factor = COPY_BYTES / (c * 1024.0)
+        out[name] = {"gemv_kib_per_dispatch": g, "copy_kib_per_dispatch": c, "copy_bytes": COPY_BYTES,
+                     "scale": factor, "gemv_bytes_per_dispatch": g * 1024.0 * factor,
+                     "n_gemv": len(gemv), "n_copy": len(copy)}
+    traffic = out["FETCH_SIZE"]["gemv_bytes_per_dispatch"] + out["WRITE_SIZE"]["gemv_bytes_per_dispatch"]
+    res = {"kernel": "k_gemv_p fused W_gate|W_up 28672x4096 (config 2)", "alg_bytes_per_launch": GATE_UP_BYTES,
+           "traffic_bytes_per_launch": round(traffic), "traffic_over_alg": round(traffic / GATE_UP_BYTES, 4),
+           "counters": out, "command": cmd}
+    p = REPO / "profiles" / "gemv_gate_up_traffic.json"
+    p.write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res))
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (profiles/gemv_gate_up_traffic.json), or None."""
@@ -346,11 +423,22 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
+    ap.add_argument("--traffic", action="store_true",
+                    help="run only the workload of the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/gemv_gate_up_traffic.json from two --pmc output dirs")
+    ap.add_argument("--traffic-cmd", default="", help="command line recorded with the summary")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic, args.traffic_cmd)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (batch-1 decode of an 8B model is not "
               f"sharded); --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
+    if args.traffic:
+        run_traffic()
+        return
 
     wall, achieved, kern_ms, breakdown = run_gpu(args)
     ms_per_step = wall / args.steps * 1e3
