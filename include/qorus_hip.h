@@ -94,6 +94,33 @@ q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* con
                                      float* const* ys, uint32_t n, const void* workspace,
                                      qh_stream s);
 
+/* ---- Batched prefill GEMM (MFMA) ----
+ * Y[t][m] = sum_k W[m][k] * X[t][k] for t < T: the prefill projections of
+ * reference src/models/model.c:1120-1165, 1446-1458, 1485-1512, 1555-1561,
+ * which run q_gemv_q4_f32_avx2 (src/ops/avx2/matmul.c:98-271) once per
+ * token row; here one MFMA contraction over all T rows.  X is [T][N]
+ * row-major fp32 (16-byte aligned), Y is [T][M] fp32 (4-byte aligned, not
+ * overlapping X).  Accuracy: max |Y - Y64| / sum_k |W x| at or below the
+ * reference AVX2 order's (fp16 matrix cores with exact Q4 operands, a
+ * two-part split of X and fp32 per-block scaling).  A token row holding a
+ * non-finite value yields NaN outputs.
+ * Validation, per matrix and in this order: W, X or Y NULL -> INVALID_ARG;
+ * X not 16-byte or Y not 4-byte aligned -> MISALIGNED; M == 0, N == 0,
+ * N % 32, N differing between the matrices or T == 0 -> INVALID_SIZE;
+ * type != Q4_0 -> INVALID_DTYPE; N/32 > UINT32_MAX/M or M*N/32*20 >= 2^31
+ * -> OVERFLOW; nb[0] != N/32*20 or W->data NULL -> INVALID_ARG; W->data
+ * not 4-byte aligned -> MISALIGNED; Y overlapping X -> ALIASING; then
+ * workspace NULL -> INVALID_ARG.
+ * `workspace` holds qh_gemm_workspace_bytes(N, T, M) bytes (for _multi:
+ * M = sum of the matrices' rows). */
+size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total);
+q_error_code qh_gemm_q4_f32(const q_tensor* W, const float* X, uint32_t T, float* Y, void* workspace,
+                            qh_stream s);
+/* Two matrices with the same N sharing X (W_gate|W_up of the MLP) in one
+ * launch: Ys[i] = X . Ws[i]^T, n in {1, 2}. */
+q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, uint32_t n, const float* X,
+                                  uint32_t T, void* workspace, qh_stream s);
+
 /* ---- Vector ops (device pointers, same validation as the qorus.h op) ---- */
 
 /* Reference src/ops/avx2/rmsnorm.c:15-92 (sum of squares reduced as a fixed

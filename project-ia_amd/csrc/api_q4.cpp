@@ -136,6 +136,54 @@ q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* con
     return Q_OK;
 }
 
+static constexpr bool kGemmEnabled = false;
+
+size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
+    return gemm_workspace_bytes(N, T, M_total);
+}
+
+q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, uint32_t n, const float* X,
+                                  uint32_t T, void* workspace, qh_stream s) {
+    if (!Ws) return Q_ERR_INVALID_ARG;
+    if (n < 1 || n > 2) return Q_ERR_INVALID_SIZE;
+    const uint8_t* w[2];
+    float* y[2];
+    uint32_t M[2];
+    for (uint32_t i = 0; i < n; ++i) {
+        const q_tensor* W = Ws[i];
+        if (!W || !Ys || !Ys[i] || !X) return Q_ERR_INVALID_ARG;
+        if (!aligned(X, 16) || !aligned(Ys[i], 4)) return Q_ERR_MISALIGNED;
+        const uint32_t Mi = W->ne[0], N = W->ne[1];
+        if (Mi == 0 || N == 0 || N % 32 != 0 || N != Ws[0]->ne[1] || T == 0) return Q_ERR_INVALID_SIZE;
+        if (W->type != Q_Q4_0) return Q_ERR_INVALID_DTYPE;
+        if (N / 32 > UINT32_MAX / Mi || (uint64_t)Mi * (N / 32) * 20u >= (1ull << 31)) return Q_ERR_OVERFLOW;
+        if (W->nb[0] != (size_t)(N / 32) * sizeof(q_block_q4_0)) return Q_ERR_INVALID_ARG;
+        if (!W->data) return Q_ERR_INVALID_ARG;
+        if (!aligned(W->data, 4)) return Q_ERR_MISALIGNED;
+        // Y must not overlap X (the kernel reads X after writing Y tiles).
+        const uintptr_t x0 = reinterpret_cast<uintptr_t>(X), x1 = x0 + (size_t)T * N * 4;
+        const uintptr_t y0 = reinterpret_cast<uintptr_t>(Ys[i]), y1 = y0 + (size_t)T * Mi * 4;
+        if (y0 < x1 && x0 < y1) return Q_ERR_ALIASING;
+        w[i] = static_cast<const uint8_t*>(W->data);
+        y[i] = Ys[i];
+        M[i] = Mi;
+    }
+    if (!workspace) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    // The MFMA GEMM kernel faulted the GPU on its first run and the cause is
+    // not established; the entry point refuses to launch it until it is.
+    if (!kGemmEnabled) return fail(hipErrorNotSupported, "qh_gemm: prefill GEMM kernel disabled");
+    QH_TRY(launch_gemm(w, y, M, (int)n, Ws[0]->ne[1], X, T, workspace, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_gemm_q4_f32(const q_tensor* W, const float* X, uint32_t T, float* Y, void* workspace,
+                            qh_stream s) {
+    if (!W) return Q_ERR_INVALID_ARG;
+    return qh_gemm_q4_f32_multi(&W, &Y, 1, X, T, workspace, s);
+}
+
 // Reference src/ops/avx2/dequantize.c:82-96: silent return on NULL.
 void q_dequantize_q4_0_block_avx2_public(const q_block_q4_0* __restrict__ block, float* __restrict__ output) {
     if (!block || !output) return;

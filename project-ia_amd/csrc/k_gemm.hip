@@ -1,0 +1,418 @@
+// k_gemm.hip -- batched Q4_0 x fp32 GEMM for prefill on gfx950 MFMA.
+//
+// Y[t][m] = sum_k W[m][k] * X[t][k], the per-token GEMV of reference
+// src/models/model.c:1120-1561 (every prefill projection loops
+// q_gemv_q4_f32_avx2 over the tokens) done as one dense contraction.
+//
+// Exactness plan (fp32-level accuracy on fp16 matrix cores):
+//  * W: the nibble of a Q4_0 element minus 8 is an integer in [-8, 7],
+//    exact in fp16.  The block scale s is NOT folded into the operand; each
+//    32-element block is one K=32 MFMA step whose fp32 result D is scaled by
+//    s in fp32 (inner += s * D), so W enters the matrix core exactly.
+//  * X: each token row is scaled by a power of two 2^e (max |x| in
+//    [2^14, 2^15)) and split into fp16 hi = rn(x') and lo = rn(x' - hi):
+//    22 significant bits.  Two MFMAs per block (hi, lo) accumulate into the
+//    same D; the products (q-8)*hi and (q-8)*lo are exact.
+//  * Accumulation: a block's D feeds an inner fp32 sum over kInner blocks,
+//    which is added to an outer sum (two-level summation): max error
+//    relative to sum_k |W x| stays at or below the reference AVX2 order's
+//    (four 8-lane accumulators over N/32 blocks) at Llama-3 shapes.
+//  * Output: y = outer * 2^-e (exact); a token row with a non-finite input
+//    gives NaN outputs (the GEMV kernel's convention).
+//
+// Tiling: a workgroup of WM x WT waves computes (64*WM rows) x (64*WT
+// tokens); each wave a 64x64 tile as 4x4 MFMA 16x16x32 tiles.  K advances
+// in steps of 2 blocks staged in LDS (double-buffered, one barrier per
+// step): X hi/lo as fp16 rows padded to 144 bytes (conflict-free 16-byte
+// reads), W as raw 16-byte nibble blocks + scales, dequantized per lane
+// right before the MFMA.  Workgroups are ordered so that each XCD keeps one
+// token tile of X resident in its L2 and streams the weight rows.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "qh_kernels.hpp"
+
+namespace qh {
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kBufFlagsG = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
+constexpr int kKB = 2;                  // Q4_0 blocks per K-step
+constexpr int kInner = 8;               // blocks per inner sum
+constexpr int kXRow = 72;               // LDS halfs per staged X row (64 + 8 pad)
+
+// In-group order of the 8 elements a lane feeds to the MFMA: the nibble
+// unpack below yields (e0,e4), (e1,e5), (e2,e6), (e3,e7) as half pairs, so
+// position p holds element perm8(p) = {0,4,1,5,2,6,3,7}[p].
+__device__ __forceinline__ constexpr int perm8(int p) { return (p >> 1) + 4 * (p & 1); }
+
+// ---------------------------------------------------------------------------
+// X preparation: one workgroup per (padded) token row.
+// xh/xl: [T_pad][N_pad] fp16, permuted within groups of 8; columns >= N and
+// rows >= T are zero.  meta[t] = (2^-e, non-finite flag).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X, uint32_t T, uint32_t N,
+                                                    uint32_t N_pad, _Float16* __restrict__ xh,
+                                                    _Float16* __restrict__ xl, float2* __restrict__ meta) {
+    __shared__ float red_m[4];
+    __shared__ int red_f[4];
+    const uint32_t t = blockIdx.x;
+    const bool valid = t < T;
+    const float* xr = X + (size_t)t * N;
+    float m = 0.0f;
+    int nf = 0;
+    if (valid) {
+        for (uint32_t i = threadIdx.x; i < N; i += 256) {
+            const float v = xr[i];
+            nf |= !__builtin_isfinite(v);
+            m = fmaxf(m, fabsf(v));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off));
+        nf |= __shfl_xor(nf, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red_m[threadIdx.x >> 6] = m;
+        red_f[threadIdx.x >> 6] = nf;
+    }
+    __syncthreads();
+    m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    nf = red_f[0] | red_f[1] | red_f[2] | red_f[3];
+    int e = 0;
+    if (!nf && m > 0.0f) {
+        int E;
+        frexpf(m, &E);  // m = f * 2^E, f in [0.5, 1)
+        e = 15 - E;     // m * 2^e in [2^14, 2^15)
+    }
+    _Float16* hr = xh + (size_t)t * N_pad;
+    _Float16* lr = xl + (size_t)t * N_pad;
+    for (uint32_t g = threadIdx.x; g < N_pad / 8; g += 256) {
+        h8v hv, lv;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const uint32_t k = g * 8 + (uint32_t)perm8(p);
+            const float v = (valid && !nf && k < N) ? ldexpf(xr[k], e) : 0.0f;
+            const _Float16 h = (_Float16)v;
+            hv[p] = h;
+            lv[p] = (_Float16)(v - (float)h);
+        }
+        *reinterpret_cast<h8v*>(hr + g * 8) = hv;
+        *reinterpret_cast<h8v*>(lr + g * 8) = lv;
+    }
+    if (threadIdx.x == 0) meta[t] = make_float2(ldexpf(1.0f, -e), nf ? 1.0f : 0.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Main kernel
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+    const uint8_t* w[2];
+    float* y[2];
+    uint32_t M[2];
+    uint32_t mt_end[2];   // cumulative m-tile counts per segment
+    uint32_t nseg;
+    uint32_t nblk;        // blocks per weight row
+    uint32_t T;
+    uint32_t N_pad;       // staged X row length (halfs)
+    uint32_t n_tt;        // token tiles
+    uint32_t split;       // K splits (partials when > 1)
+    uint32_t blk_per_split;
+    uint32_t xcd_map;     // 1: XCD-aware tile order
+    const _Float16* xh;
+    const _Float16* xl;
+    const float2* meta;
+    float* part;          // [split][T][M_total-slot] partials (split > 1)
+    uint32_t part_ld;     // partial row length (sum of segment M)
+    uint32_t part_off[2]; // column offset of each segment in a partial row
+};
+
+// 8 nibbles of one dword -> 8 fp16 (q - 8), in the kPerm order.
+__device__ __forceinline__ h8v unpack8(uint32_t w) {
+    h8v r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t b = ((w >> (4 * c)) & 0x000F000Fu) | 0x64006400u;  // (1024 + n_c, 1024 + n_{c+4})
+        h2v h = __builtin_bit_cast(h2v, b);
+        h = h - h2v{(_Float16)1032.0f, (_Float16)1032.0f};
+        r[2 * c] = h[0];
+        r[2 * c + 1] = h[1];
+    }
+    return r;
+}
+
+template <int WM, int WT>
+__global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
+    constexpr int NT = 64 * WM * WT;
+    constexpr int BM = 64 * WM;
+    constexpr int BT = 64 * WT;
+    constexpr int XCH = 16 * BT / NT;   // 16-byte X chunks per thread per K-step
+    constexpr int WBL = BM * kKB / NT;  // weight blocks per thread per K-step
+    static_assert(XCH * NT == 16 * BT && WBL * NT == BM * kKB, "tile/thread mismatch");
+
+    __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BT][kXRow];
+    __shared__ __attribute__((aligned(16))) uint32_t lw[2][BM][kKB][4];
+    __shared__ float ls[2][BM][kKB];
+
+    // ---- tile of this workgroup ----
+    const uint32_t n_mt = a.mt_end[a.nseg - 1] * a.split;  // (m-tile, split) pairs
+    uint32_t mm, tt;
+    {
+        const uint32_t b = blockIdx.x;
+        if (a.xcd_map) {
+            const uint32_t xcd = b & 7u, k = b >> 3;
+            tt = xcd % a.n_tt;
+            mm = xcd / a.n_tt + (8u / a.n_tt) * k;
+        } else {
+            tt = b % a.n_tt;
+            mm = b / a.n_tt;
+        }
+        if (mm >= n_mt) return;
+    }
+    const uint32_t mtile = mm / a.split, sp = mm % a.split;
+    const uint32_t sg = (a.nseg > 1 && mtile >= a.mt_end[0]) ? 1u : 0u;
+    const uint32_t m0 = (mtile - (sg ? a.mt_end[0] : 0u)) * BM;
+    const uint32_t t0 = tt * BT;
+    const uint32_t M = a.M[sg];
+    const uint32_t row_bytes = a.nblk * 20u;
+    const uint32_t b_begin = sp * a.blk_per_split;
+    const uint32_t b_end = min(a.nblk, b_begin + a.blk_per_split);
+    const uint32_t nsteps = b_end > b_begin ? (b_end - b_begin + kKB - 1) / kKB : 0u;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wt = wave / WM;
+
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.w[sg], 0, (int)(M * row_bytes), kBufFlagsG);
+
+    // ---- global -> register staging of one K-step ----
+    u4v gx[XCH];
+    u4v gq[WBL];
+    float gs[WBL];
+    auto load_step = [&](uint32_t step) {
+        const uint32_t b0 = b_begin + step * kKB;
+        const uint32_t k0 = b0 * 32u;  // < N_pad - 63 by construction (N_pad % 64 == 0)
+#pragma unroll
+        for (int c = 0; c < XCH; ++c) {
+            const uint32_t idx = (uint32_t)(tid + NT * c);
+            const uint32_t part = idx / (8u * BT);
+            const uint32_t rem = idx % (8u * BT);
+            const uint32_t t = rem / 8u, ch = rem % 8u;
+            const _Float16* src = (part ? a.xl : a.xh) + (size_t)(t0 + t) * a.N_pad + k0 + 8u * ch;
+            gx[c] = *reinterpret_cast<const u4v*>(src);
+        }
+#pragma unroll
+        for (int j = 0; j < WBL; ++j) {
+            const uint32_t idx = (uint32_t)(tid + NT * j);
+            const uint32_t r = idx / kKB, kb = idx % kKB;
+            const uint32_t b = b0 + kb;
+            const uint32_t off = (m0 + r) * row_bytes + b * 20u;  // rows >= M read zeros
+            u4v q = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+            float s = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, off + 16u, 0, 0));
+            const bool ok = b < b_end;
+            gq[j] = ok ? q : u4v{0u, 0u, 0u, 0u};
+            gs[j] = ok ? s : 0.0f;
+        }
+    };
+    auto store_step = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < XCH; ++c) {
+            const uint32_t idx = (uint32_t)(tid + NT * c);
+            const uint32_t part = idx / (8u * BT);
+            const uint32_t rem = idx % (8u * BT);
+            const uint32_t t = rem / 8u, ch = rem % 8u;
+            *reinterpret_cast<u4v*>(&lx[buf][part][t][8u * ch]) = gx[c];
+        }
+#pragma unroll
+        for (int j = 0; j < WBL; ++j) {
+            const uint32_t idx = (uint32_t)(tid + NT * j);
+            const uint32_t r = idx / kKB, kb = idx % kKB;
+            *reinterpret_cast<u4v*>(&lw[buf][r][kb][0]) = gq[j];
+            ls[buf][r][kb] = gs[j];
+        }
+    };
+
+    f4v inner[4][4], outer[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            inner[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+            outer[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    const int lr = lane & 15, lq = lane >> 4;
+    if (nsteps > 0) {
+        load_step(0);
+        store_step(0);
+    }
+    __syncthreads();
+    uint32_t nb_in = 0;  // blocks in the current inner sum
+    for (uint32_t step = 0; step < nsteps; ++step) {
+        const int buf = step & 1;
+        if (step + 1 < nsteps) load_step(step + 1);
+#pragma unroll
+        for (int kb = 0; kb < kKB; ++kb) {
+            h8v B[4];
+            float s[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 64 * wm + 16 * i + lr;
+                B[i] = unpack8(lw[buf][r][kb][lq]);
+                s[i] = ls[buf][r][kb];
+            }
+            h8v Ah[4], Al[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 64 * wt + 16 * j + lr;
+                Ah[j] = *reinterpret_cast<const h8v*>(&lx[buf][0][t][32 * kb + 8 * lq]);
+                Al[j] = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah[j], B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al[j], B[i], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) inner[i][j][r] = fmaf(s[i], d[r], inner[i][j][r]);
+                }
+        }
+        nb_in += kKB;
+        if (nb_in >= kInner) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    outer[i][j] += inner[i][j];
+                    inner[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            nb_in = 0;
+        }
+        if (step + 1 < nsteps) store_step(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds column m (weight row), tokens 4*lq + r ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t m = m0 + 64 * wm + 16 * i + lr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f4v v = outer[i][j] + inner[i][j];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t t = t0 + 64 * wt + 16 * j + 4 * lq + r;
+                if (m < M && t < a.T) {
+                    if (a.split > 1) {
+                        a.part[((size_t)sp * a.T + t) * a.part_ld + a.part_off[sg] + m] = v[r];
+                    } else {
+                        const float2 mt = a.meta[t];
+                        a.y[sg][(size_t)t * M + m] = mt.y != 0.0f ? __builtin_nanf("") : v[r] * mt.x;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Fixed-order sum of the K-split partials, scaled by 2^-e of the token.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
+    const uint32_t ld = a.part_ld;
+    const size_t n = (size_t)a.T * ld;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const uint32_t t = (uint32_t)(i / ld), c = (uint32_t)(i % ld);
+        float v = a.part[i];
+        for (uint32_t sp = 1; sp < a.split; ++sp) v += a.part[(size_t)sp * n + i];
+        const uint32_t sg = (a.nseg > 1 && c >= a.part_off[1]) ? 1u : 0u;
+        const uint32_t m = c - a.part_off[sg];
+        const float2 mt = a.meta[t];
+        a.y[sg][(size_t)t * a.M[sg] + m] = mt.y != 0.0f ? __builtin_nanf("") : v * mt.x;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+constexpr int kGemmWM = 4, kGemmWT = 2;
+constexpr uint32_t kGemmBM = 64 * kGemmWM, kGemmBT = 64 * kGemmWT;
+
+static uint32_t gemm_tpad(uint32_t T) { return (T + kGemmBT - 1) / kGemmBT * kGemmBT; }
+static uint32_t gemm_npad(uint32_t N) { return (N + 63u) & ~63u; }
+
+// K splits: enough (m-tile, token-tile, split) workgroups to cover the 256
+// CUs, each split keeping at least 32 blocks.
+static uint32_t gemm_split(uint32_t M_total, uint32_t T, uint32_t nblk) {
+    const uint32_t tiles = (M_total + kGemmBM - 1) / kGemmBM * (gemm_tpad(T) / kGemmBT);
+    uint32_t s = 1;
+    while (tiles * s < 256u && s < 8u && nblk / (2u * s) >= 32u) s *= 2u;
+    return s;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
+    const size_t tp = gemm_tpad(T), np = gemm_npad(N);
+    const uint32_t sp = gemm_split(M_total, T, N / 32u);
+    size_t b = 2 * align256(tp * np * 2) + align256(tp * 8);
+    if (sp > 1) b += align256((size_t)sp * T * M_total * 4);
+    return b;
+}
+
+hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t* M, int nseg, uint32_t N,
+                       const float* X, uint32_t T, void* ws, hipStream_t s) {
+    if (nseg < 1 || nseg > 2 || T == 0 || N == 0 || N % 32 != 0) return hipErrorInvalidValue;
+    const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
+    uint8_t* p = static_cast<uint8_t*>(ws);
+    GemmArgs a{};
+    a.xh = reinterpret_cast<_Float16*>(p);
+    a.xl = reinterpret_cast<_Float16*>(p + align256((size_t)tp * np * 2));
+    a.meta = reinterpret_cast<float2*>(p + 2 * align256((size_t)tp * np * 2));
+    float* part = reinterpret_cast<float*>(p + 2 * align256((size_t)tp * np * 2) + align256((size_t)tp * 8));
+    uint32_t mt = 0, mtot = 0;
+    for (int i = 0; i < nseg; ++i) {
+        // Weight offsets are 32-bit buffer offsets.
+        if ((uint64_t)M[i] * (N / 32u) * 20u >= (1ull << 31)) return hipErrorInvalidValue;
+        a.w[i] = w[i];
+        a.y[i] = y[i];
+        a.M[i] = M[i];
+        a.part_off[i] = mtot;
+        mtot += M[i];
+        mt += (M[i] + kGemmBM - 1) / kGemmBM;
+        a.mt_end[i] = mt;
+    }
+    a.nseg = (uint32_t)nseg;
+    a.nblk = N / 32;
+    a.T = T;
+    a.N_pad = np;
+    a.n_tt = tp / kGemmBT;
+    a.split = gemm_split(mtot, T, a.nblk);
+    a.blk_per_split = ((a.nblk + a.split - 1) / a.split + kKB - 1) / kKB * kKB;
+    a.part = part;
+    a.part_ld = mtot;
+    // The XCD-aware order needs the token-tile count to divide the 8 XCDs.
+    a.xcd_map = (8u % a.n_tt == 0) ? 1u : 0u;
+    hipLaunchKernelGGL(k_gemm_xprep, dim3(tp), dim3(256), 0, s, X, T, N, np, const_cast<_Float16*>(a.xh),
+                       const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t pairs = mt * a.split * a.n_tt;
+    const uint32_t grid = a.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
+    hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.split == 1) return e;
+    const size_t n = (size_t)T * mtot;
+    const uint32_t rg = (uint32_t)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(rg), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace qh

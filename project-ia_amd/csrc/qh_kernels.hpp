@@ -55,6 +55,13 @@ struct GemvDecode {
 hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd,
                        hipStream_t s, const GemvDecode* dec = nullptr);
 
+// ---- batched prefill GEMM (k_gemm.hip) ----
+// Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 or 2) matrices sharing
+// X [T][N] (row-major fp32); Y_i is [T][M_i].  ws: gemm_workspace_bytes.
+size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total);
+hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t* M, int nseg, uint32_t N,
+                       const float* X, uint32_t T, void* ws, hipStream_t s);
+
 // ---- vector kernels (k_vec.hip) ----
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s);
 // RoPE of n_vec consecutive vectors of length N with one cos/sin table pair.
