@@ -326,6 +326,130 @@ def run_cpu_decode(path, kv, first_tok, gpu_tok0, n_tokens):
 
 
 # ---------------------------------------------------------------------------
+# LM head + softmax + argmax
+# ---------------------------------------------------------------------------
+VOCAB = 128256
+LM_COPIES = 2  # 2 x 328 MB: more than the 256 MB MALL holds
+
+
+def lmhead_bytes():
+    """Algorithmic HBM bytes of one config-3 step: the Q4_0 LM head once,
+    x, the logits written and read back by softmax and argmax, the
+    probabilities written."""
+    return alg_bytes(VOCAB, DIM) + 3 * 4 * VOCAB
+
+
+def run_lmhead(args):
+    import qorus_amd as qa
+    from qorus_amd import synthetic as syn
+    lib = qa.lib()
+    rng = syn.rng_for(4242)
+    Ws = [qa.DeviceBuffer.from_numpy(syn.gen_q4(VOCAB, DIM, rng)) for _ in range(LM_COPIES)]
+    ts = [qa.q4_tensor(w.ptr, VOCAB, DIM) for w in Ws]
+    x = qa.DeviceBuffer.from_numpy(syn.gen_f32(DIM, rng))
+    ws = qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(DIM))
+    logits, probs = qa.DeviceBuffer(VOCAB * 4), qa.DeviceBuffer(VOCAB * 4)
+    tok = qa.DeviceBuffer(4)
+    stream = qa.Stream()
+    s = stream.handle
+    ys = ptr_array([logits.ptr])
+
+    def gemv(t):
+        qa.check(lib.qh_gemv_prepare(x.ptr, DIM, ws.ptr, s))
+        qa.check(lib.qh_gemv_q4_f32_prepared(ptr_array([t.addr]), None, ys, 1, ws.ptr, s))
+
+    def softmax():
+        qa.check(lib.qh_softmax_f32(logits.ptr, probs.ptr, VOCAB, s))
+
+    def argmax():
+        qa.check(lib.qh_argmax_f32(logits.ptr, VOCAB, tok.ptr, s))
+
+    graphs = []
+    for t in ts:
+        qa.check(lib.qh_stream_begin_capture(s))
+        gemv(t)
+        softmax()
+        argmax()
+        g = C.c_void_p()
+        qa.check(lib.qh_stream_end_capture(s, C.byref(g)))
+        graphs.append(g.value)
+    steps = max(10, args.steps // 4)
+    for i in range(8):
+        qa.check(lib.qh_graph_launch(graphs[i % LM_COPIES], s))
+    stream.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        qa.check(lib.qh_graph_launch(graphs[i % LM_COPIES], s))
+    stream.sync()
+    wall = time.perf_counter() - t0
+    # correctness spot check: the device argmax is the host argmax
+    lg = logits.download(np.float32, (VOCAB,))
+    tk = int(tok.download(np.uint32, (1,))[0])
+    ok = tk == int(np.argmax(lg))
+    # stage timings with events (eager launches on the same stream)
+    stages = {"gemv": [], "softmax": [], "argmax": []}
+    for i in range(16):
+        for name, fn in (("gemv", lambda: gemv(ts[i % LM_COPIES])), ("softmax", softmax), ("argmax", argmax)):
+            a, b = qa.Event(), qa.Event()
+            a.record(stream)
+            fn()
+            b.record(stream)
+            stream.sync()
+            stages[name].append(a.elapsed_ms(b))
+    for g in graphs:
+        lib.qh_graph_destroy(g)
+    ms = wall / steps * 1e3
+    nbytes = lmhead_bytes()
+    cpu = None if args.no_cpu else run_cpu_lmhead()
+    return {"workload": "config3: LM head 128256x4096 Q4_0 GEMV + softmax over 128256 logits + argmax, "
+                        "hipGraph per step, 2 rotated weight copies",
+            "ms_per_step": round(ms, 5), "steps": steps, "alg_bytes": nbytes,
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "stage_us": {k: round(float(np.median(v)) * 1e3, 2) for k, v in stages.items()},
+            "argmax_matches_host": ok, "cpu_baseline": cpu}
+
+
+def run_cpu_lmhead(n_steps=3):
+    """Config 3 on one pinned host core: the reference's own
+    q_gemv_q4_f32_avx2 and q_softmax_f32_avx2 (oracle/_ref) plus the
+    oracle's argmax, n_steps times on one synthetic LM head."""
+    from oracle import oracle as orc
+    if not orc.ref_available():
+        return None
+    from qorus_amd import synthetic as syn
+    R = orc.ref()
+    rng = syn.rng_for(4243)
+    W = orc.aligned_copy(syn.gen_q4(VOCAB, DIM, rng).reshape(-1))
+    x = orc.aligned_copy(syn.gen_f32(DIM, rng))
+    lg = orc.aligned_empty((VOCAB,), np.float32)
+    pr = orc.aligned_empty((VOCAB,), np.float32)
+    t = orc.q4_tensor(W.ctypes.data, VOCAB, DIM)
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        def step():
+            assert R.q_gemv_q4_f32_avx2(C.addressof(t[0]), x.ctypes.data, lg.ctypes.data) == 0
+            assert R.q_softmax_f32_avx2(lg.ctypes.data, pr.ctypes.data, VOCAB) == 0
+            orc.argmax(lg)
+        step()
+        t0 = time.perf_counter()
+        for _ in range(n_steps):
+            step()
+        el = time.perf_counter() - t0
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    return {"value": round(n_steps / el, 3), "unit": "steps/s", "ms_per_step": round(el / n_steps * 1e3, 2),
+            "cores": 1, "kind": "reference",
+            "sample": f"{n_steps} steps of the reference's q_gemv_q4_f32_avx2 (128256x4096) + q_softmax_f32_avx2 "
+                      f"+ argmax on 1 pinned core ({orc.cpu_model_name()})"}
+
+
+# ---------------------------------------------------------------------------
 # HBM traffic of the dominant kernel (rocprofv3 --pmc passes)
 # ---------------------------------------------------------------------------
 COPY_BYTES = 256 << 20
@@ -423,6 +547,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
+    ap.add_argument("--no-lmhead", action="store_true", help="skip the config-3 LM-head leg")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -444,6 +569,7 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = STEP_BYTES * args.steps / wall / 1e9
     cpu = None if args.no_cpu else run_cpu_baseline(args.cpu_seconds)
+    lmhead = None if args.no_lmhead else run_lmhead(args)
     decode = None if args.no_decode else run_decode(args)
     out = {
         "metric": METRIC,
@@ -469,6 +595,7 @@ def main():
                      "alg_bytes_per_launch": GATE_UP_BYTES, "mean_launch_us": round(kern_ms * 1e3, 2)},
         "kernels": breakdown,
         "cpu_baseline": cpu,
+        "lmhead": lmhead,
         "decode": decode,
     }
     print(json.dumps(out), flush=True)

@@ -75,6 +75,17 @@ q_error_code q_gemv_q4_f32_avx2(const q_tensor* Q_RESTRICT weights,
                                 const float* Q_RESTRICT input,
                                 float* Q_RESTRICT output);
 
+/* C[M x N] = A[M x K] . B[K x N], fp32; B may be a transposed view
+ * (nb[0] == 4, ne[0] > 1, nb[1] > 4: element (k, j) at B->data[j*K + k]).
+ * Same validation order and codes as the reference; a non-transposed B
+ * takes N*K*4 bytes from ctx's arena (the reference's transpose buffer,
+ * -> Q_ERR_ARENA_OOM when it does not fit).  Host pointers, synchronous;
+ * every dot product follows the reference's accumulation order exactly.
+ * Replaces reference qorus.h:84-89 / src/ops/avx2/matmul_fp32.c:57-474. */
+q_error_code q_matmul_f32_avx2(const q_tensor* Q_RESTRICT A,
+                               const q_tensor* Q_RESTRICT B, q_tensor* C,
+                               q_context* Q_RESTRICT ctx);
+
 /* out = a + b (1-D, in-place allowed).
  * Replaces reference qorus.h:109-113 / src/ops/avx2/add_fp32.c:17-164. */
 q_error_code q_add_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output);

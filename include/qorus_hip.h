@@ -138,13 +138,22 @@ q_error_code qh_silu_f32(const float* x, float* output, uint32_t N, qh_stream s)
 q_error_code qh_silu_mul_f32(const float* gate, const float* up, float* output, uint32_t N,
                              qh_stream s);
 /* Reference src/ops/avx2/softmax.c:17-132 (sum reduced as a fixed tree);
- * x may alias output. */
+ * x may alias output.  For N >= 16384 the work is spread over many
+ * workgroups whose partial results live in a workspace: qh_softmax_f32
+ * uses one library workspace per process (calls that may overlap on
+ * different streams must use qh_softmax_f32_ws with a workspace of
+ * qh_softmax_workspace_bytes(N) device bytes each). */
 q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream s);
+size_t qh_softmax_workspace_bytes(uint32_t N);
+q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* workspace, qh_stream s);
 q_error_code qh_add_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s);
 q_error_code qh_mul_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s);
 /* Greedy argmax of reference src/main.c:870-881 (first index of the
- * maximum); writes the index to device memory *index_out. */
+ * maximum); writes the index to device memory *index_out.  Workspace rules
+ * as for softmax (qh_argmax_f32_ws / qh_argmax_workspace_bytes). */
 q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_stream s);
+size_t qh_argmax_workspace_bytes(uint32_t N);
+q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, void* workspace, qh_stream s);
 
 /* ---- Decode on the device ---- */
 

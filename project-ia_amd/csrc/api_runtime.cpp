@@ -41,6 +41,7 @@ q_error_code device(Device** out) {
         Device* d = new Device();
         d->id = id;
         QH_TRY(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+        QH_TRY(hipMalloc(reinterpret_cast<void**>(&d->reduce_ws), kReduceWsBytes));
         g_dev = d;
     }
     *out = g_dev;

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdio>
 #include <mutex>
 
 #include "qh_kernels.hpp"
@@ -116,6 +117,58 @@ using namespace qh;
 
 extern "C" {
 
+// Reference src/ops/avx2/matmul_fp32.c:57-300, validation in its order:
+// NULL A/B/C/ctx -> INVALID_ARG; M, K or N zero, B->ne[0] != K, C->ne[0] !=
+// M, C->ne[1] != N -> INVALID_SIZE; A->nb[0] % 32 == 0 with A->data not
+// 32-byte aligned -> MISALIGNED (reported on stderr, as the reference
+// does); any type != F32 -> INVALID_DTYPE; row strides below K (A), N (B)
+// or the transposed B's column stride below K, or C's below N ->
+// INVALID_SIZE; a non-transposed B then takes its N*K*4-byte transpose
+// buffer from the arena (NULL -> ARENA_OOM).
+q_error_code q_matmul_f32_avx2(const q_tensor* __restrict__ A, const q_tensor* __restrict__ B, q_tensor* C,
+                               q_context* __restrict__ ctx) {
+    if (!A || !B || !C || !ctx) return Q_ERR_INVALID_ARG;
+    const uint32_t M = A->ne[0], K = A->ne[1], N = B->ne[1];
+    if (M == 0 || K == 0 || N == 0) return Q_ERR_INVALID_SIZE;
+    if (B->ne[0] != K || C->ne[0] != M || C->ne[1] != N) return Q_ERR_INVALID_SIZE;
+    if (A->nb[0] % 32 == 0 && reinterpret_cast<uintptr_t>(A->data) % 32 != 0) {
+        fprintf(stderr, "ERROR: q_matmul_f32_avx2: A->data not 32-byte aligned: %p\n", A->data);
+        return Q_ERR_MISALIGNED;
+    }
+    if (A->type != Q_F32 || B->type != Q_F32 || C->type != Q_F32) return Q_ERR_INVALID_DTYPE;
+    const size_t lda = A->nb[0] / sizeof(float), ldb = B->nb[0] / sizeof(float), ldc = C->nb[0] / sizeof(float);
+    if (lda < K) return Q_ERR_INVALID_SIZE;
+    const bool bt = B->nb[0] == sizeof(float) && B->ne[0] > 1 && B->nb[1] > sizeof(float);
+    if (bt) {
+        if (B->nb[1] / sizeof(float) < K) return Q_ERR_INVALID_SIZE;
+    } else if (ldb < N) {
+        return Q_ERR_INVALID_SIZE;
+    }
+    if (ldc < N) return Q_ERR_INVALID_SIZE;
+    if (!bt && !q_arena_alloc(ctx, (size_t)N * K * sizeof(float))) return Q_ERR_ARENA_OOM;
+
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, Stager::round((size_t)M * K * 4) + Stager::round((size_t)K * N * 4) +
+                               Stager::round((size_t)M * N * 4)));
+    float* dA = st.take((size_t)M * K);
+    float* dB = st.take((size_t)K * N);
+    float* dC = st.take((size_t)M * N);
+    hipStream_t s = d->stream;
+    // Compact device copies of exactly the elements the reference reads.
+    QH_TRY(hipMemcpy2DAsync(dA, (size_t)K * 4, A->data, lda * 4, (size_t)K * 4, M, hipMemcpyHostToDevice, s));
+    if (bt)
+        QH_TRY(hipMemcpyAsync(dB, B->data, (size_t)N * K * 4, hipMemcpyHostToDevice, s));
+    else
+        QH_TRY(hipMemcpy2DAsync(dB, (size_t)N * 4, B->data, ldb * 4, (size_t)N * 4, K, hipMemcpyHostToDevice, s));
+    QH_TRY(launch_matmul_f32(dA, K, dB, bt ? K : N, bt, dC, N, M, N, K, s));
+    QH_TRY(hipMemcpy2DAsync(C->data, ldc * 4, dC, (size_t)N * 4, (size_t)N * 4, M, hipMemcpyDeviceToHost, s));
+    QH_TRY(hipStreamSynchronize(s));
+    return Q_OK;
+}
+
 q_error_code q_rmsnorm_f32_avx2(const float* __restrict__ x, const float* __restrict__ weight,
                                 float* __restrict__ output, uint32_t N, float eps) {
     QH_TRY_CODE(validate_rmsnorm(x, weight, output, N));
@@ -175,7 +228,7 @@ q_error_code q_softmax_f32_avx2(const float* __restrict__ x, float* __restrict__
     QH_TRY_CODE(st.open(d, Stager::round((size_t)N * 4)));
     float* dx = st.take(N);
     QH_TRY_CODE(st.put(dx, x, N));
-    QH_TRY(launch_softmax(dx, dx, N, d->stream));
+    QH_TRY(launch_softmax_ws(dx, dx, N, d->reduce_ws, d->stream));
     return st.get(output, dx, N);
 }
 
@@ -228,7 +281,19 @@ q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream
     QH_TRY_CODE(validate_softmax(x, output, N));
     Device* d;
     QH_TRY_CODE(device(&d));
-    QH_TRY(launch_softmax(x, output, N, (hipStream_t)s));
+    QH_TRY(launch_softmax_ws(x, output, N, d->reduce_ws, (hipStream_t)s));
+    return Q_OK;
+}
+
+size_t qh_softmax_workspace_bytes(uint32_t N) { return softmax_workspace_bytes(N); }
+size_t qh_argmax_workspace_bytes(uint32_t N) { return argmax_workspace_bytes(N); }
+
+q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* workspace, qh_stream s) {
+    QH_TRY_CODE(validate_softmax(x, output, N));
+    if (!workspace) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_softmax_ws(x, output, N, static_cast<float*>(workspace), (hipStream_t)s));
     return Q_OK;
 }
 
@@ -253,7 +318,17 @@ q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_s
     if (N == 0) return Q_ERR_INVALID_SIZE;
     Device* d;
     QH_TRY_CODE(device(&d));
-    QH_TRY(launch_argmax(x, N, index_out, (hipStream_t)s));
+    QH_TRY(launch_argmax_ws(x, N, index_out, nullptr, nullptr, nullptr, 0, d->reduce_ws, (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, void* workspace, qh_stream s) {
+    if (!x || !index_out || !workspace) return Q_ERR_INVALID_ARG;
+    if (N == 0) return Q_ERR_INVALID_SIZE;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_argmax_ws(x, N, index_out, nullptr, nullptr, nullptr, 0, static_cast<float*>(workspace),
+                            (hipStream_t)s));
     return Q_OK;
 }
 

@@ -28,16 +28,23 @@ constexpr int kHd = 128;      // head_dim this build's attention kernels are wri
 constexpr int kChunk = 64;    // keys per workgroup
 constexpr uint32_t kMaxGroup = 8;  // q heads per kv head (1, 2, 4 or 8)
 
-// Reference dot order for K = 128 (matmul_fp32.c:356-425): 32 partial sums,
-// lane (c, l) = (lane/8, lane%8) of a 32-lane half accumulating terms
-// k = 32t + 8c + l for t = 0..3 with FMA, then (a0+a1)+(a2+a3) per l, then
-// ((S0+S4)+(S1+S5))+((S2+S6)+(S3+S7)).  The full dot ends in lane 0 of the half.
-__device__ __forceinline__ float dot_tree32(float acc) {
-    const float v01 = acc + __shfl_xor(acc, 8, 32);   // c=0: a0+a1, c=2: a2+a3
-    const float s = v01 + __shfl_xor(v01, 16, 32);    // c=0: (a0+a1)+(a2+a3)
-    const float t = s + __shfl_xor(s, 4, 32);         // l<4: S_l + S_{l+4}
-    const float u = t + __shfl_xor(t, 1, 32);         // l=0: T0+T1, l=2: T2+T3
-    return u + __shfl_xor(u, 2, 32);                  // l=0: (T0+T1)+(T2+T3)
+// Reference dot order for K = 128 (matmul_fp32.c:356-425): 32 partial sums
+// a[c][l] (c = 0..3 accumulators, l = 0..7 lanes), element k = 32t + 8c + l
+// accumulated over t = 0..3 with FMA; S_l = (a0+a1)+(a2+a3); then
+// ((S0+S4)+(S1+S5))+((S2+S6)+(S3+S7)).  Here 8 consecutive lanes compute
+// one dot: lane l holds a[0..3][l], forms S_l locally, and the last tree runs
+// on DPP (row_shl:4 pairs l with l+4, then quad_perm swaps 1 and 2), so the
+// sum takes the reference's pairs bit for bit without LDS round trips.  The
+// dot ends in lane l = 0 of each group of 8.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float dot_tree8(float s) {
+    const float t = s + dpp_f<0x104>(s);  // row_shl:4: l < 4 -> S_l + S_{l+4}
+    const float u = t + dpp_f<0xB1>(t);   // quad_perm [1,0,3,2]: l=0 -> T0+T1, l=2 -> T2+T3
+    return u + dpp_f<0x4E>(u);            // quad_perm [2,3,0,1]: l=0 -> (T0+T1)+(T2+T3)
 }
 
 template <uint32_t group>
@@ -52,46 +59,59 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     if (j0 >= S) return;
     __shared__ float smax[4][kMaxGroup];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int half = lane >> 5, c = (lane >> 3) & 3, l = lane & 7;
-    // q values this lane multiplies: q[h][32t + 8c + l], t = 0..3
-    float qv[group][4];
+    const int g = lane >> 3, l = lane & 7;  // key slot g of the pass, reference lane l
+    // q values this lane multiplies: q[h][32t + 8c + l]
+    float qv[group][4][4];
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) qv[h][t] = q[(size_t)(kvh * group + h) * kHd + 32 * t + 8 * c + l];
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qv[h][c][t] = q[(size_t)(kvh * group + h) * kHd + 32 * t + 8 * c + l];
     float mx[group];
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) mx[h] = -INFINITY;
     const float* kbase = kv + (size_t)kvh * head_stride;
-    // 64 keys per workgroup: each wave takes 16, two per step (one per half);
-    // all 8 steps' key values are loaded before any is used.
-    float kk[8][4];
+    // 64 keys per workgroup: each wave takes 16 in two passes of 8 (one key
+    // per 8-lane group); both passes' key values are loaded before any use.
+    float kk[2][4][4];
 #pragma unroll
-    for (int step = 0; step < 8; ++step) {
-        const uint32_t j = j0 + (uint32_t)(wave * 16 + step * 2 + half);
+    for (int ps = 0; ps < 2; ++ps) {
+        const uint32_t j = j0 + (uint32_t)(wave * 16 + ps * 8 + g);
         const float* krow = kbase + (size_t)(j < S ? j : 0u) * (2 * kHd);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kk[step][t] = krow[32 * t + 8 * c + l];
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) kk[ps][c][t] = krow[32 * t + 8 * c + l];
     }
 #pragma unroll
-    for (int step = 0; step < 8; ++step) {
-        const uint32_t j = j0 + (uint32_t)(wave * 16 + step * 2 + half);
+    for (int ps = 0; ps < 2; ++ps) {
+        const uint32_t j = j0 + (uint32_t)(wave * 16 + ps * 8 + g);
         const bool valid = j < S;
 #pragma unroll
         for (uint32_t h = 0; h < group; ++h) {
-            float acc = 0.0f;
+            float a[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc = fmaf(qv[h][t], kk[step][t], acc);
-            const float d = dot_tree32(acc);
+            for (int c = 0; c < 4; ++c) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc = fmaf(qv[h][c][t], kk[ps][c][t], acc);
+                a[c] = acc;
+            }
+            const float sl = (a[0] + a[1]) + (a[2] + a[3]);
+            const float d = dot_tree8(sl);
             const float sc = d * scale;
-            if (valid && (lane & 31) == 0) scores[(size_t)(kvh * group + h) * max_seq + j] = sc;
+            if (valid && l == 0) scores[(size_t)(kvh * group + h) * max_seq + j] = sc;
             if (valid) mx[h] = fmaxf(mx[h], sc);
         }
     }
-    // per-head max over the chunk (lane 0 of each half holds its keys' max)
+    // per-head max over the chunk: lanes l = 0 hold their keys' values; the
+    // max is exact, so any combination order gives the same result.
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) {
-        float m = fmaxf(mx[h], __shfl_xor(mx[h], 32));
+        float m = (l == 0) ? mx[h] : -INFINITY;
+#pragma unroll
+        for (int off = 8; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
         if (lane == 0) smax[wave][h] = m;
     }
     __syncthreads();
@@ -118,6 +138,29 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
     __shared__ float o_s[kMaxGroup][kHd];
     __shared__ float gmax[kMaxGroup];
     const uint32_t tid = threadIdx.x;
+    // Loads that do not depend on the global max are issued first: this
+    // chunk's V rows (thread (hf, d): keys hf*32 .. hf*32+31, element d) and
+    // its scores.  Keys past S read a clamped, in-bounds row and are zeroed.
+    const uint32_t d = tid % kHd, hf = tid / kHd;
+    const float* vbase = kv + (size_t)kvh * head_stride + kHd;
+    float vv[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+        const uint32_t j = j0 + hf * 32 + (uint32_t)u;
+        const float v = vbase[(size_t)(j < S ? j : S - 1u) * (2 * kHd) + d];
+        vv[u] = (j < S) ? v : 0.0f;
+    }
+    constexpr uint32_t kPer = (group * kChunk + 255) / 256;
+    float scv[kPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kPer; ++r) {
+        const uint32_t i = tid + 256 * r;
+        const uint32_t h = i / kChunk, jj = i % kChunk, j = j0 + jj;
+        const bool ok = i < group * kChunk && j < S;
+        const uint32_t hc = h < group ? h : 0u;
+        const float sv = scores[(size_t)(kvh * group + hc) * max_seq + (j < S ? j : S - 1u)];
+        scv[r] = ok ? sv : 0.0f;
+    }
     // Global max per head: one wave per head (lane-strided loads, then a
     // butterfly max); exact, so the order does not matter.
     {
@@ -133,14 +176,18 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
     }
     __syncthreads();
     // e_j for the chunk's keys and all group heads.
-    for (uint32_t i = tid; i < group * kChunk; i += 256) {
-        const uint32_t h = i / kChunk, jj = i % kChunk, j = j0 + jj;
-        float e = 0.0f;
-        if (j < S) {
-            const float d = scores[(size_t)(kvh * group + h) * max_seq + j] - gmax[h];
-            e = (j < Sv) ? exp_approx(d) : expf(d);
+#pragma unroll
+    for (uint32_t r = 0; r < kPer; ++r) {
+        const uint32_t i = tid + 256 * r;
+        if (i < group * kChunk) {
+            const uint32_t h = i / kChunk, jj = i % kChunk, j = j0 + jj;
+            float e = 0.0f;
+            if (j < S) {
+                const float dd = scv[r] - gmax[h];
+                e = (j < Sv) ? exp_approx(dd) : expf(dd);
+            }
+            e_s[h][jj] = e;
         }
-        e_s[h][jj] = e;
     }
     __syncthreads();
     if (tid < group) {
@@ -148,17 +195,15 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
         for (int jj = 0; jj < kChunk; ++jj) sum += e_s[tid][jj];
         part_sum[(size_t)(kvh * group + tid) * n_chunks + chunk] = sum;
     }
-    // P.V partials: thread (half, d) over 32 keys, all group heads.
-    const uint32_t d = tid % kHd, hf = tid / kHd;
+    // P.V partials: thread (half, d) over its 32 keys, all group heads.
     float acc[group];
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) acc[h] = 0.0f;
-    const float* vbase = kv + (size_t)kvh * head_stride + kHd;
-    for (int jj = (int)hf * 32; jj < (int)hf * 32 + 32; ++jj) {
-        const uint32_t j = j0 + (uint32_t)jj;
-        const float v = (j < S) ? vbase[(size_t)j * (2 * kHd) + d] : 0.0f;
 #pragma unroll
-        for (uint32_t h = 0; h < group; ++h) acc[h] = fmaf(e_s[h][jj], v, acc[h]);
+    for (int u = 0; u < 32; ++u) {
+        const int jj = (int)hf * 32 + u;
+#pragma unroll
+        for (uint32_t h = 0; h < group; ++h) acc[h] = fmaf(e_s[h][jj], vv[u], acc[h]);
     }
     if (hf == 1)
 #pragma unroll
@@ -186,23 +231,25 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     if (valid) {
         const uint32_t h = t / kHd;
         float total = 0.0f, acc = 0.0f;
-        uint32_t c = 0;
-        for (; c + 8 <= nch; c += 8) {
-            float ps[8], op[8];
+        // Rounds of 32 chunks with every load of a round in flight together
+        // (indices clamped in bounds, contributions past nch zeroed); the
+        // sums stay sequential in chunk order.
+        for (uint32_t c0 = 0; c0 < nch; c0 += 32) {
+            float ps[32], op[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                ps[u] = part_sum[(size_t)h * n_chunks + c + u];
-                op[u] = o_part[(size_t)(c + u) * N + t];
+            for (int u = 0; u < 32; ++u) {
+                const uint32_t c = c0 + (uint32_t)u;
+                const uint32_t cc = c < nch ? c : nch - 1u;
+                ps[u] = part_sum[(size_t)h * n_chunks + cc];
+                op[u] = o_part[(size_t)cc * N + t];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                total += ps[u];
-                acc += op[u];
+            for (int u = 0; u < 32; ++u) {
+                if (c0 + (uint32_t)u < nch) {
+                    total += ps[u];
+                    acc += op[u];
+                }
             }
-        }
-        for (; c < nch; ++c) {
-            total += part_sum[(size_t)h * n_chunks + c];
-            acc += o_part[(size_t)c * N + t];
         }
         if (S < 8) {
             v = acc / total;

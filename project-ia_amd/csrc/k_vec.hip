@@ -19,6 +19,9 @@
 
 namespace qh {
 
+constexpr uint32_t kSmxSlice = 2048;       // elements per workgroup slice (multi-workgroup path)
+constexpr uint32_t kSmxMaxSlices = 1024;   // slices are widened beyond this many
+constexpr uint32_t kSmxMultiMin = 16384;   // below this N one workgroup is faster
 constexpr int kVecThreads = 1024;
 
 // RMSNorm, one workgroup of 256 threads: y = (x*r)*w (reference
@@ -140,6 +143,87 @@ hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Multi-workgroup softmax for large N (same semantics as k_softmax, N >= 8):
+//   A: per-slice max over all N elements;
+//   B: global max (exact, any order), e_i = exp_approx(x_i - m) for i <
+//      N&~7 written to y with a per-slice fixed-order sum; tail e_i =
+//      expf(x_i - m) written to y and kept in the workspace;
+//   C: total = per-slice sums in slice order, then the tail values in index
+//      order; inv = 1/total; y_i *= inv.
+// Workspace floats: [0, G) slice max, [G, 2G) slice sums, [2G, 2G+8) tail.
+__global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uint32_t slice, float* ws) {
+    __shared__ float red[4];
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    float m = -INFINITY;
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) m = fmaxf(m, x[i]);
+    m = block_max<256>(m, red);
+    if (threadIdx.x == 0) ws[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint32_t N, uint32_t slice, uint32_t G,
+                                                 float* ws) {
+    __shared__ float red[4];
+    float m = -INFINITY;
+    for (uint32_t g = threadIdx.x; g < G; g += 256) m = fmaxf(m, ws[g]);
+    m = block_max<256>(m, red);
+    const uint32_t nv = N & ~7u;
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    float ls = 0.0f;
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
+        const float d = x[i] - m;
+        if (i < nv) {
+            const float e = exp_approx(d);
+            ls = ls + e;
+            y[i] = e;
+        } else {
+            const float e = expf(d);
+            y[i] = e;
+            ws[2 * G + (i - nv)] = e;
+        }
+    }
+    const float sum = block_sum<256>(ls, red);
+    if (threadIdx.x == 0) ws[G + blockIdx.x] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_smx_norm(float* y, uint32_t N, uint32_t slice, uint32_t G,
+                                                  const float* ws) {
+    __shared__ float inv_s;
+    if (threadIdx.x == 0) {
+        float total = 0.0f;
+        for (uint32_t g = 0; g < G; ++g) total = total + ws[G + g];
+        for (uint32_t i = (N & ~7u); i < N; ++i) total = total + ws[2 * G + (i - (N & ~7u))];
+        inv_s = 1.0f / total;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) y[i] = y[i] * inv;
+}
+
+static void smx_shape(uint32_t N, uint32_t* slice, uint32_t* G) {
+    uint32_t sl = kSmxSlice;
+    while ((N + sl - 1) / sl > kSmxMaxSlices) sl *= 2;
+    *slice = sl;
+    *G = (N + sl - 1) / sl;
+}
+
+size_t softmax_workspace_bytes(uint32_t N) {
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    return ((size_t)4 * G + 8) * sizeof(float);
+}
+
+hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    if (N < kSmxMultiMin || !ws) return launch_softmax(x, y, N, s);
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
+    return hipGetLastError();
+}
+
 // Elementwise add / mul (reference add_fp32.c:127-161, mul_fp32.c:89-123).
 __global__ __launch_bounds__(256) void k_binary(const float* a, const float* b, float* o, uint32_t N, int op) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -233,6 +317,186 @@ hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t 
 hipError_t launch_argmax_step(const float* x, uint32_t N, uint32_t* tok_out, uint32_t* pos_inout, uint32_t* hist,
                               uint32_t* hist_n, uint32_t hist_cap, hipStream_t s) {
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, tok_out, pos_inout, hist, hist_n, hist_cap);
+    return hipGetLastError();
+}
+
+// Multi-workgroup argmax: per-slice (value, first index) partials, then one
+// workgroup combines them.  arg_better is a total order on non-NaN values
+// (larger value, then smaller index), so the result does not depend on the
+// combination order; NaN never wins, and a NaN at index 0 gives index 0 (no
+// element compares greater than it, reference main.c:870-881).
+// Workspace: floats [0, G) values, then uint32 [G, 2G) indices.
+__global__ __launch_bounds__(256) void k_amax_part(const float* __restrict__ x, uint32_t N, uint32_t slice,
+                                                   float* __restrict__ ws) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
+        const float v = x[i];
+        if (arg_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (arg_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = sv[0];
+        uint32_t i = si[0];
+        for (int k = 1; k < 4; ++k)
+            if (arg_better(sv[k], si[k], v, i)) {
+                v = sv[k];
+                i = si[k];
+            }
+        ws[blockIdx.x] = v;
+        reinterpret_cast<uint32_t*>(ws)[gridDim.x + blockIdx.x] = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_amax_final(const float* __restrict__ x, uint32_t N, uint32_t G,
+                                                    const float* __restrict__ ws, uint32_t* __restrict__ out,
+                                                    uint32_t* __restrict__ pos_inout, uint32_t* __restrict__ hist,
+                                                    uint32_t* __restrict__ hist_n, uint32_t hist_cap) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const uint32_t* wi = reinterpret_cast<const uint32_t*>(ws) + G;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t g = threadIdx.x; g < G; g += 256) {
+        const float v = ws[g];
+        const uint32_t i = wi[g];
+        if (arg_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (arg_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = sv[0];
+        uint32_t i = si[0];
+        for (int k = 1; k < 4; ++k)
+            if (arg_better(sv[k], si[k], v, i)) {
+                v = sv[k];
+                i = si[k];
+            }
+        if (x[0] != x[0]) i = 0;  // NaN at index 0: nothing compares greater
+        if (i == 0xFFFFFFFFu) i = 0;
+        *out = i;
+        if (pos_inout) *pos_inout += 1u;
+        if (hist) {
+            const uint32_t n = *hist_n;
+            if (n < hist_cap) hist[n] = i;
+            *hist_n = n + 1u;
+        }
+    }
+}
+
+size_t argmax_workspace_bytes(uint32_t N) {
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    return (size_t)2 * G * sizeof(float);
+}
+
+hipError_t launch_argmax_ws(const float* x, uint32_t N, uint32_t* out, uint32_t* pos_inout, uint32_t* hist,
+                            uint32_t* hist_n, uint32_t hist_cap, float* ws, hipStream_t s) {
+    if (N < kSmxMultiMin || !ws) {
+        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kVecThreads), 0, s, x, N, out, pos_inout, hist, hist_n, hist_cap);
+        return hipGetLastError();
+    }
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    hipLaunchKernelGGL(k_amax_part, dim3(G), dim3(256), 0, s, x, N, sl, ws);
+    hipLaunchKernelGGL(k_amax_final, dim3(1), dim3(256), 0, s, x, N, G, ws, out, pos_inout, hist, hist_n, hist_cap);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fp32 matmul C = A . B in the reference dot order (matmul_fp32.c:302-468):
+// per 32-element chunk of K, element k goes to accumulator c = (k%32)/8,
+// lane l = k%8, with FMA; per lane S_l = (a0+a1)+(a2+a3); then
+// ((S0+S4)+(S1+S5))+((S2+S6)+(S3+S7)) (hsum256_ps); then the K%32 tail
+// sequentially as dot = dot + a*b (separately rounded).  Eight lanes per
+// output element: lane l holds a[0..3][l]; the tree runs on DPP.
+// B element (k, j) is B[k*ldb + j], or B[j*K + k] when bt (a transposed
+// view, read with column stride K as the reference does).
+// ---------------------------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ float dpp_sel(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__global__ __launch_bounds__(256) void k_matmul_f32(const float* __restrict__ A, uint32_t lda,
+                                                    const float* __restrict__ B, uint32_t ldb, uint32_t bt,
+                                                    float* __restrict__ C, uint32_t ldc, uint32_t M, uint32_t N,
+                                                    uint32_t K) {
+    const uint64_t gid = ((uint64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    const uint32_t l = threadIdx.x & 7;
+    const bool valid = gid < (uint64_t)M * N;
+    // Every lane of a group takes part in the DPP tree; a group past the end
+    // computes element (0, 0) and does not store.
+    const uint32_t i = valid ? (uint32_t)(gid / N) : 0u;
+    const uint32_t j = valid ? (uint32_t)(gid % N) : 0u;
+    const float* a = A + (size_t)i * lda;
+    const float* bcol = bt ? B + (size_t)j * K : B + j;
+    const size_t bstep = bt ? 1 : ldb;
+    const uint32_t kv = K & ~31u;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k = 0; k < kv; k += 32) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t kk = k + 8u * c + l;
+            acc[c] = fmaf(a[kk], bcol[(size_t)kk * bstep], acc[c]);
+        }
+    }
+    const float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const float t = s + dpp_sel<0x104>(s);  // row_shl:4: l < 4 -> S_l + S_{l+4}
+    const float u = t + dpp_sel<0xB1>(t);   // quad_perm [1,0,3,2]
+    const float d = u + dpp_sel<0x4E>(u);   // quad_perm [2,3,0,1]: lane 0 holds the tree
+    if (valid && l == 0) {
+        float dot = kv > 0 ? d : 0.0f;
+        for (uint32_t k = kv; k < K; ++k) {
+            const float p = a[k] * bcol[(size_t)k * bstep];
+            dot = dot + p;
+        }
+        C[(size_t)i * ldc + j] = dot;
+    }
+}
+
+hipError_t launch_matmul_f32(const float* A, uint32_t lda, const float* B, uint32_t ldb, bool bt, float* C,
+                             uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, hipStream_t s) {
+    const uint64_t threads = (uint64_t)M * N * 8;
+    const uint64_t grid = (threads + 255) / 256;
+    if (grid == 0) return hipSuccess;
+    if (grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_matmul_f32, dim3((uint32_t)grid), dim3(256), 0, s, A, lda, B, ldb, bt ? 1u : 0u, C, ldc,
+                       M, N, K);
     return hipGetLastError();
 }
 

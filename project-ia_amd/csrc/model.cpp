@@ -31,8 +31,6 @@
 
 namespace qh {
 
-hipError_t launch_argmax_step(const float* x, uint32_t N, uint32_t* tok_out, uint32_t* pos_inout,
-                              uint32_t* hist, uint32_t* hist_n, uint32_t hist_cap, hipStream_t s);  // k_vec.hip
 
 struct LayerDev {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
@@ -57,6 +55,7 @@ struct ModelPlan {
     float *cos_tab = nullptr, *sin_tab = nullptr;
     uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
     uint32_t hist_cap = 0;
+    float* amax_ws = nullptr;                // multi-workgroup argmax partials
     float* kv = nullptr;
     size_t kv_layer_floats = 0;
     hipStream_t stream = nullptr;
@@ -196,7 +195,8 @@ static hipError_t enqueue_step(ModelPlan* p, bool feedback) {
     QH_E(launch_xprep(p->x, c.dim, p->out_norm, c.rms_norm_eps, nullptr, p->xd_a, s));
     GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
     QH_E(launch_gemv(&lm, 1, nblk_d, p->xd_a, s));
-    if (feedback) QH_E(launch_argmax_step(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, s));
+    if (feedback)
+        QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->amax_ws, s));
 #undef QH_E
     return hipSuccess;
 }
@@ -410,6 +410,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     const size_t o_op = carve(nch * cfg.n_heads * hd * 4);
     const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
     const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
+    const size_t o_aw = carve(argmax_workspace_bytes(cfg.vocab_size));
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
@@ -440,6 +441,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->pos = reinterpret_cast<uint32_t*>(A + o_pos);
     p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
+    p->amax_ws = reinterpret_cast<float*>(A + o_aw);
     st->plan = p;
     st->dev_arena = p->arena;
     st->dev_arena_size = bytes;

@@ -73,5 +73,18 @@ hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s);
 // op 0: o = a + b; op 1: o = a * b.
 hipError_t launch_binary(const float* a, const float* b, float* o, uint32_t N, int op, hipStream_t s);
 hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t s);
+// Multi-workgroup softmax / argmax for large N with a device workspace of
+// softmax_workspace_bytes(N) / argmax_workspace_bytes(N) bytes (ws may be
+// null, or N small: then the one-workgroup kernels run).  The argmax form
+// also advances *pos_inout and appends to hist when those are non-null.
+size_t softmax_workspace_bytes(uint32_t N);
+size_t argmax_workspace_bytes(uint32_t N);
+hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hipStream_t s);
+hipError_t launch_argmax_ws(const float* x, uint32_t N, uint32_t* out, uint32_t* pos_inout, uint32_t* hist,
+                            uint32_t* hist_n, uint32_t hist_cap, float* ws, hipStream_t s);
+// C[M x N] (row stride ldc) = A (row stride lda) . B, B[k*ldb + j] or, with
+// bt, B[j*K + k]; reference dot order.
+hipError_t launch_matmul_f32(const float* A, uint32_t lda, const float* B, uint32_t ldb, bool bt, float* C,
+                             uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, hipStream_t s);
 
 }  // namespace qh

@@ -40,7 +40,12 @@ struct Device {
     // Grow-only device staging used by the host-pointer entry points.
     void* stage[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t stage_bytes[4] = {0, 0, 0, 0};
+    // Partials of the multi-workgroup softmax/argmax used by the entry points
+    // that take no workspace (allocated once at initialization).
+    float* reduce_ws = nullptr;
 };
+
+constexpr size_t kReduceWsBytes = 32768;
 
 // Returns Q_OK and the initialized device, or an error if no GPU is usable.
 q_error_code device(Device** out);

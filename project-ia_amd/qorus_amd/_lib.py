@@ -152,12 +152,17 @@ def lib():
     _sig(L, "q_silu_f32_avx2", i32, vp, vp, u32)
     _sig(L, "q_softmax_f32_avx2", i32, vp, vp, u32)
     _sig(L, "q_add_f32_avx2", i32, vp, vp, vp)
+    _sig(L, "q_matmul_f32_avx2", i32, vp, vp, vp, vp)
     _sig(L, "q_mul_f32_avx2", i32, vp, vp, vp)
     _sig(L, "qh_rmsnorm_f32", i32, vp, vp, vp, u32, f32, vp)
     _sig(L, "qh_rope_f32", i32, vp, vp, vp, vp, u32, u32, vp)
     _sig(L, "qh_silu_f32", i32, vp, vp, u32, vp)
     _sig(L, "qh_silu_mul_f32", i32, vp, vp, vp, u32, vp)
     _sig(L, "qh_softmax_f32", i32, vp, vp, u32, vp)
+    _sig(L, "qh_softmax_workspace_bytes", C.c_size_t, u32)
+    _sig(L, "qh_softmax_f32_ws", i32, vp, vp, u32, vp, vp)
+    _sig(L, "qh_argmax_workspace_bytes", C.c_size_t, u32)
+    _sig(L, "qh_argmax_f32_ws", i32, vp, u32, vp, vp, vp)
     _sig(L, "qh_add_f32", i32, vp, vp, vp, u32, vp)
     _sig(L, "qh_mul_f32", i32, vp, vp, vp, u32, vp)
     _sig(L, "qh_argmax_f32", i32, vp, u32, vp, vp)

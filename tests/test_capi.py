@@ -187,3 +187,40 @@ def test_model_file_layout_agrees_with_oracle(tmp_path):
     olay = orc.model_layout(hd)
     for k, v in lay.items():
         assert olay[k] == v, k
+
+
+def test_matmul_f32_validation_order():
+    """q_matmul_f32_avx2 error codes in the reference's order
+    (matmul_fp32.c:64-285); all of these return before any device work."""
+    import ctypes as C
+    import numpy as np
+    from oracle import oracle as orc
+    from qorus_amd._lib import _AlignedTensor
+    from qorus_amd.model import QContext
+    lib = L.lib()
+    A = orc.aligned_empty((4, 64), np.float32)
+    B = orc.aligned_empty((64, 8), np.float32)
+    Cm = orc.aligned_empty((4, 8), np.float32)
+
+    def T(arr, ne0, ne1, nb0, nb1=4, dtype=None, off=0):
+        return _AlignedTensor(arr.ctypes.data + off, (ne0, ne1, 1, 1), (nb0, nb1, 4, 4),
+                              L.Q_F32 if dtype is None else dtype)
+
+    ctx = QContext()
+    ta, tb, tc = T(A, 4, 64, 256), T(B, 64, 8, 32), T(Cm, 4, 8, 32)
+    f = lambda a, b, c, x: lib.q_matmul_f32_avx2(a.addr if a else None, b.addr if b else None,
+                                                 c.addr if c else None, C.byref(x) if x is not None else None)
+    assert f(None, tb, tc, ctx) == -10
+    assert f(ta, tb, tc, None) == -10
+    assert f(T(A, 0, 64, 256), tb, tc, ctx) == -15          # M == 0
+    assert f(ta, T(B, 63, 8, 32), tc, ctx) == -15           # B->ne[0] != K
+    assert f(ta, tb, T(Cm, 4, 7, 32), ctx) == -15           # C->ne[1] != N
+    assert f(T(A, 4, 64, 256, off=4), tb, tc, ctx) == -13   # A->data misaligned with aligned stride
+    assert f(ta, T(B, 64, 8, 32, dtype=L.Q_Q4_0), tc, ctx) == -14
+    assert f(T(A, 4, 64, 128), tb, tc, ctx) == -15          # A stride < K
+    assert f(ta, T(B, 64, 8, 16), tc, ctx) == -15           # B stride < N
+    assert f(ta, tb, T(Cm, 4, 8, 16), ctx) == -15           # C stride < N
+    assert f(ta, tb, tc, ctx) == -8                         # no arena for the transpose buffer
+    # a misaligned A with an unaligned stride is accepted by validation
+    # (then the transpose buffer is the first failure here)
+    assert f(T(A, 4, 60, 244, off=4), T(B, 60, 8, 32), tc, ctx) == -8

@@ -130,3 +130,131 @@ def test_argmax(qa):
         qa.check(qa.lib().qh_argmax_f32(dx.ptr, x.size, out.ptr, None))
         qa.check(qa.lib().qh_device_synchronize())
         assert int(out.download(np.uint32, (1,))[0]) == orc.argmax(x)
+
+
+def test_argmax_multi_workgroup_cases(qa):
+    """N >= 16384 takes the multi-workgroup path (per-slice partials, then a
+    combine): ties across slices keep the first index, NaN never wins, NaN
+    at index 0 gives 0, all -inf gives 0; _ws form with its own workspace."""
+    lib = qa.lib()
+    N = 128256
+    rng = orc.rng_for(209)
+    base = orc.gen_f32(N, rng)
+    tie = base.copy()
+    tie[[5000, 70000, 127000]] = 50.0                 # tie across three slices
+    nan_mid = base.copy()
+    nan_mid[[3, 64000]] = np.nan
+    nan_mid[90000] = 60.0
+    nan0 = base.copy()
+    nan0[0] = np.nan
+    cases = [base, tie, nan_mid, nan0, np.full(N, -np.inf, np.float32), np.zeros(N, np.float32),
+             np.concatenate([np.full(N - 1, -1.0, np.float32), [np.float32(-0.5)]])]
+    out = qa.DeviceBuffer(4)
+    ws = qa.DeviceBuffer(lib.qh_argmax_workspace_bytes(N))
+    for x in cases:
+        dx = qa.DeviceBuffer.from_numpy(x)
+        for use_ws in (False, True):
+            if use_ws:
+                qa.check(lib.qh_argmax_f32_ws(dx.ptr, N, out.ptr, ws.ptr, None))
+            else:
+                qa.check(lib.qh_argmax_f32(dx.ptr, N, out.ptr, None))
+            qa.check(lib.qh_device_synchronize())
+            assert int(out.download(np.uint32, (1,))[0]) == orc.argmax(x)
+
+
+@pytest.mark.parametrize("N", [16384, 128256, 131077, 3000000])
+def test_softmax_multi_workgroup(qa, N):
+    """Device softmax on the multi-workgroup path (N % 8 tails included),
+    with and without an explicit workspace, in place and out of place."""
+    lib = qa.lib()
+    rng = orc.rng_for(211, N)
+    x = (orc.gen_f32(N, rng) * 3).astype(np.float32)
+    want = orc.softmax(orc.aligned_copy(x))
+    dx = qa.DeviceBuffer.from_numpy(x)
+    dy = qa.DeviceBuffer(N * 4)
+    ws = qa.DeviceBuffer(lib.qh_softmax_workspace_bytes(N))
+    for mode in ("plain", "ws", "inplace"):
+        if mode == "plain":
+            qa.check(lib.qh_softmax_f32(dx.ptr, dy.ptr, N, None))
+        elif mode == "ws":
+            qa.check(lib.qh_softmax_f32_ws(dx.ptr, dy.ptr, N, ws.ptr, None))
+        else:
+            dz = qa.DeviceBuffer.from_numpy(x)
+            qa.check(lib.qh_softmax_f32_ws(dz.ptr, dz.ptr, N, ws.ptr, None))
+            dy = dz
+        qa.check(lib.qh_device_synchronize())
+        y = dy.download(np.float32, (N,))
+        assert np.array_equal(y == 0, want == 0)
+        nz = want != 0
+        assert np.max(np.abs(y[nz] - want[nz]) / want[nz]) <= 2e-6
+
+
+# ------------------------------------------------------------ fp32 matmul --
+
+def _mat_tensor(qa, arr, ne0, ne1, nb0, nb1=4):
+    from qorus_amd._lib import _AlignedTensor
+    return _AlignedTensor(arr.ctypes.data, (ne0, ne1, 1, 1), (nb0, nb1, 4, 4), qa.Q_F32)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 2048), (32, 128, 33), (5, 31, 7), (3, 33, 4), (7, 200, 9),
+                                   (64, 1024, 64), (1, 1, 1)])
+def test_matmul_f32_bitexact(qa, M, K, N):
+    """q_matmul_f32_avx2 (reference matmul_fp32.c): dense, transposed-B and
+    strided variants, bit-exact with the oracle's restatement (itself
+    bit-identical to the reference build, see test_oracle)."""
+    import ctypes as C
+    from qorus_amd.model import QContext
+    lib = qa.lib()
+    rng = orc.rng_for(M * 1000 + K, N)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = rng.standard_normal((K, N), dtype=np.float32)
+    want = orc.matmul_f32(A, B)
+    ctx = QContext()
+    assert lib.q_alloc_arena(C.byref(ctx), K * N * 4 + 4096) == 0
+    try:
+        # dense
+        Aa, Ba = orc.aligned_copy(A), orc.aligned_copy(B)
+        Cc = orc.aligned_empty((M, N), np.float32)
+        ta, tb, tc = _mat_tensor(qa, Aa, M, K, K * 4), _mat_tensor(qa, Ba, K, N, N * 4), _mat_tensor(qa, Cc, M, N, N * 4)
+        assert lib.q_matmul_f32_avx2(ta.addr, tb.addr, tc.addr, C.byref(ctx)) == 0
+        assert np.array_equal(bits(Cc), bits(want))
+        # transposed B view: element (k, j) at Bt[j*K + k]; no arena use
+        Bt = orc.aligned_copy(np.ascontiguousarray(B.T))
+        head = ctx.scratch_head
+        tbt = _mat_tensor(qa, Bt, K, N, 4, K * 4)
+        Ct = orc.aligned_empty((M, N), np.float32)
+        tct = _mat_tensor(qa, Ct, M, N, N * 4)
+        assert lib.q_matmul_f32_avx2(ta.addr, tbt.addr, tct.addr, C.byref(ctx)) == 0
+        if K > 1:
+            assert ctx.scratch_head == head
+            assert np.array_equal(bits(Ct), bits(want))
+        # strided A (row stride K+5 floats) and C (row stride N+3): gaps untouched
+        As = orc.aligned_empty((M, K + 5), np.float32)
+        As[:, :K] = A
+        As[:, K:] = np.nan
+        Cs = orc.aligned_copy(np.full((M, N + 3), 7.0, np.float32))
+        tas = _mat_tensor(qa, As, M, K, (K + 5) * 4)
+        tcs = _mat_tensor(qa, Cs, M, N, (N + 3) * 4)
+        lib.q_arena_reset(C.byref(ctx))
+        assert lib.q_matmul_f32_avx2(tas.addr, tb.addr, tcs.addr, C.byref(ctx)) == 0
+        assert np.array_equal(bits(Cs[:, :N]), bits(want))
+        assert np.all(Cs[:, N:] == 7.0)
+    finally:
+        lib.q_free_memory(C.byref(ctx))
+
+
+def test_matmul_f32_arena_oom(qa):
+    import ctypes as C
+    from qorus_amd.model import QContext
+    lib = qa.lib()
+    M, K, N = 4, 64, 64
+    A = orc.aligned_copy(np.ones((M, K), np.float32))
+    B = orc.aligned_copy(np.ones((K, N), np.float32))
+    Cc = orc.aligned_empty((M, N), np.float32)
+    ctx = QContext()
+    assert lib.q_alloc_arena(C.byref(ctx), 1024) == 0
+    try:
+        ta, tb, tc = _mat_tensor(qa, A, M, K, K * 4), _mat_tensor(qa, B, K, N, N * 4), _mat_tensor(qa, Cc, M, N, N * 4)
+        assert lib.q_matmul_f32_avx2(ta.addr, tb.addr, tc.addr, C.byref(ctx)) == -8  # ARENA_OOM
+    finally:
+        lib.q_free_memory(C.byref(ctx))
