@@ -152,49 +152,6 @@ struct GemvArgs {
     const float* sin_tab;
 };
 
-// Integer dots of R*J blocks (already loaded) against the x digit planes,
-// accumulated into acc[0..R): plane by plane across all blocks, each plane a
-// 4-deep dot8 chain of its own, planes combined by P = (P << 4) + S_p, so
-// the independent chains of different blocks interleave; then
-// acc += ldexp(fma(s, (float)P, z), -k) per block.
-template <int R, int J>
-__device__ __forceinline__ void dot_batch(const uint4 (&q)[R][J], const float (&s)[R][J], const uint4 (&xp)[J][6],
-                                          const int (&kk)[J], const float (&zz)[J], const bool (&ok)[J],
-                                          float (&acc)[R]) {
-    int P[R][J];
-    uint32_t wq[R][J][4];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            wq[r][j][0] = q[r][j].x ^ 0x88888888u;
-            wq[r][j][1] = q[r][j].y ^ 0x88888888u;
-            wq[r][j][2] = q[r][j].z ^ 0x88888888u;
-            wq[r][j][3] = q[r][j].w ^ 0x88888888u;
-            P[r][j] = 0;
-        }
-#pragma unroll
-    for (int p = 5; p >= 0; --p)
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                int sp = __builtin_amdgcn_sdot8((int)wq[r][j][0], (int)xp[j][p].x, 0, false);
-                sp = __builtin_amdgcn_sdot8((int)wq[r][j][1], (int)xp[j][p].y, sp, false);
-                sp = __builtin_amdgcn_sdot8((int)wq[r][j][2], (int)xp[j][p].z, sp, false);
-                sp = __builtin_amdgcn_sdot8((int)wq[r][j][3], (int)xp[j][p].w, sp, false);
-                P[r][j] = (int)((uint32_t)P[r][j] << 4) + sp;
-            }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const float sc = ok[j] ? s[r][j] : 0.0f;
-            const float c = fmaf(sc, (float)P[r][j], zz[j]);
-            acc[r] += ldexpf(c, -kk[j]);
-        }
-}
-
 // Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
 __device__ __forceinline__ void seg_of(const GemvArgs& a, uint32_t t, uint32_t& sg, uint32_t& tbase) {
     sg = 0;

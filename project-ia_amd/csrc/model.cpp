@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "qh_decode.hpp"
+#include "qh_fused.hpp"
 #include "qh_kernels.hpp"
 #include "qh_runtime.hpp"
 
@@ -56,6 +57,8 @@ struct ModelPlan {
     uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
     uint32_t hist_cap = 0;
     float* amax_ws = nullptr;                // multi-workgroup argmax partials
+    float *part_a = nullptr, *part_b = nullptr;  // per-block sums of squares of the RMSNorm inputs
+    bool fused = false;                      // 7-kernel layers (k_fused.hip)
     float* kv = nullptr;
     size_t kv_layer_floats = 0;
     hipStream_t stream = nullptr;
@@ -131,7 +134,121 @@ static q_tensor* make_view(q_context* ctx, size_t offset, uint32_t n0, uint32_t 
 // ---------------------------------------------------------------------------
 // Decode step enqueue (all kernels on p->stream)
 // ---------------------------------------------------------------------------
+// One decode step with the fused kernels: per layer QKV(+norm scale, RoPE,
+// KV store), attention (3 kernels), Wo(+residual, next norm's digits),
+// gate|up(+norm scale, SwiGLU, digits), down(+residual, next norm's digits).
+static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
+    const q_llama_config& c = p->cfg;
+    hipStream_t s = p->stream;
+    hipError_t e;
+#define QH_E(x)                          \
+    do {                                 \
+        e = (x);                         \
+        if (e != hipSuccess) return e;   \
+    } while (0)
+    const uint32_t nblk_d = c.dim / 32, nblk_h = c.hidden_dim / 32;
+    QH_E(launch_embed_prep(p->embd, p->tok, c.vocab_size, c.dim, p->layers[0].attn_norm, p->x, p->xd_a, p->part_a, s));
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const LayerDev& L = p->layers[l];
+        float* kvl = p->kv + (size_t)l * p->kv_layer_floats;
+        FusedArgs fq;
+        fq.w[0] = L.wq;
+        fq.w[1] = L.wk;
+        fq.w[2] = L.wv;
+        fq.M[0] = c.dim;
+        fq.M[1] = p->kvd;
+        fq.M[2] = p->kvd;
+        fq.nseg = 3;
+        fq.nblk = nblk_d;
+        fq.pad = xd_pad(nblk_d);
+        fq.xd = p->xd_a;
+        fq.in_part = p->part_a;
+        fq.eps = c.rms_norm_eps;
+        fq.y[0] = p->q;
+        fq.y[1] = kvl;
+        fq.y[2] = kvl + p->hd;
+        for (int i = 0; i < 3; ++i) fq.hd[i] = p->hd;
+        fq.head_stride[0] = p->hd;
+        fq.head_stride[1] = fq.head_stride[2] = c.max_seq_len * 2 * p->hd;
+        fq.pos_stride[1] = fq.pos_stride[2] = 2 * p->hd;
+        fq.rope_mask = 3u;
+        fq.pos = p->pos;
+        fq.cos_tab = p->cos_tab;
+        fq.sin_tab = p->sin_tab;
+        QH_E(launch_fused_qkv(fq, s));
+        AttnArgs aa;
+        aa.q = p->q;
+        aa.kv_layer = kvl;
+        aa.pos = p->pos;
+        aa.n_heads = c.n_heads;
+        aa.n_kv = c.n_kv_heads;
+        aa.head_dim = p->hd;
+        aa.max_seq = c.max_seq_len;
+        aa.scale = p->scale;
+        aa.scores = p->scores;
+        aa.part_max = p->part_max;
+        aa.part_sum = p->part_sum;
+        aa.o_part = p->o_part;
+        aa.o_out = nullptr;
+        aa.xd_out = p->xd_b;
+        QH_E(launch_attention(aa, s));
+        FusedArgs fo;
+        fo.w[0] = L.wo;
+        fo.M[0] = c.dim;
+        fo.nblk = nblk_d;
+        fo.pad = xd_pad(nblk_d);
+        fo.xd = p->xd_b;
+        fo.y[0] = p->x1;
+        fo.res = p->x;
+        fo.wnorm = L.ffn_norm;
+        fo.xd_out = p->xd_a;
+        fo.pad_out = xd_pad(nblk_d);
+        fo.out_part = p->part_b;
+        QH_E(launch_fused_resid(fo, s));
+        FusedArgs fg;
+        fg.w[0] = L.wg;
+        fg.w[1] = L.wu;
+        fg.M[0] = fg.M[1] = c.hidden_dim;
+        fg.nblk = nblk_d;
+        fg.pad = xd_pad(nblk_d);
+        fg.xd = p->xd_a;
+        fg.in_part = p->part_b;
+        fg.eps = c.rms_norm_eps;
+        fg.xd_out = p->xd_c;
+        fg.pad_out = xd_pad(nblk_h);
+        QH_E(launch_fused_swiglu(fg, s));
+        FusedArgs fd;
+        fd.w[0] = L.wd;
+        fd.M[0] = c.dim;
+        fd.nblk = nblk_h;
+        fd.pad = xd_pad(nblk_h);
+        fd.xd = p->xd_c;
+        fd.y[0] = p->x;
+        fd.res = p->x1;
+        fd.wnorm = (l + 1 < c.n_layers) ? p->layers[l + 1].attn_norm : p->out_norm;
+        fd.xd_out = p->xd_a;
+        fd.pad_out = xd_pad(nblk_d);
+        fd.out_part = p->part_a;
+        QH_E(launch_fused_resid(fd, s));
+    }
+    FusedArgs fl;
+    fl.w[0] = p->lm_head;
+    fl.M[0] = c.vocab_size;
+    fl.nblk = nblk_d;
+    fl.pad = xd_pad(nblk_d);
+    fl.xd = p->xd_a;
+    fl.in_part = p->part_a;
+    fl.eps = c.rms_norm_eps;
+    fl.y[0] = p->logits;
+    QH_E(launch_fused_logits(fl, s));
+    if (feedback)
+        QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->amax_ws, s));
+#undef QH_E
+    return hipSuccess;
+}
+
 static hipError_t enqueue_step(ModelPlan* p, bool feedback) {
+    if (p->fused) return enqueue_step_fused(p, feedback);
     const q_llama_config& c = p->cfg;
     hipStream_t s = p->stream;
     hipError_t e;
@@ -411,6 +528,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
     const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
     const size_t o_aw = carve(argmax_workspace_bytes(cfg.vocab_size));
+    const size_t o_pa = carve(cfg.dim / 32 * 4), o_pb = carve(cfg.dim / 32 * 4);
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
@@ -442,6 +560,10 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
     p->amax_ws = reinterpret_cast<float*>(A + o_aw);
+    p->part_a = reinterpret_cast<float*>(A + o_pa);
+    p->part_b = reinterpret_cast<float*>(A + o_pb);
+    p->fused = fused_supported(cfg.dim / 32) && fused_supported(cfg.hidden_dim / 32) && cfg.dim / 32 <= 128 &&
+               cfg.hidden_dim % 32 == 0 && cfg.dim % 32 == 0 && (p->kvd % 32) == 0;
     st->plan = p;
     st->dev_arena = p->arena;
     st->dev_arena_size = bytes;
