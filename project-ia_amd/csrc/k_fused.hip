@@ -126,17 +126,11 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
     uint4 xp[J][6];
     int kk[J];
     float zz[J];
+    {
+        uint32_t cols[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const uint32_t cc = coff[j] / 20u;
-#pragma unroll
-        for (int p = 0; p < 6; ++p) {
-            const uint4 v = a.xd[(size_t)p * a.pad + cc];
-            xp[j][p] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
-        }
-        const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
-        kk[j] = ok[j] ? (int)meta.x : 0;
-        zz[j] = ok[j] ? __uint_as_float(meta.y) : 0.0f;
+        for (int j = 0; j < J; ++j) cols[j] = coff[j] / 20u;
+        load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
     }
     float rs_norm = 1.0f;
     if (MODE != kModeResid) rs_norm = norm_scale(a.in_part, a.nblk, a.eps);
@@ -210,6 +204,112 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
     }
 }
 
+// Persistent W_gate|W_up + SwiGLU: 8 waves of 8 rows walk 64-row tiles (32
+// gate rows + the same 32 up rows).  Each wave's rows are two halves of 4;
+// the next half's loads are issued before the current half is computed (a
+// one-half-tile pipeline that needs only two 4-row buffers).  Tiles past the
+// end read zeros through size-0 buffer resources.
+template <int J>
+__global__ __launch_bounds__(512) void k_swiglu_p(const FusedArgs a, uint32_t ntiles) {
+    constexpr int RH = 4;  // rows per half
+    __shared__ float red[64];
+    const int lane = threadIdx.x & 63;
+    const int rg = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // 0..7, 8 rows each
+    const uint32_t sg = (rg >= 4) ? 1u : 0u;
+    const uint32_t roff = (uint32_t)((rg * 8) & 31);
+    const uint32_t M = a.M[0];
+    const uint32_t row_bytes = a.nblk * 20u;
+    const uint8_t* __restrict__ wseg = a.w[sg];
+
+    uint32_t coff[J];
+    bool ok[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t col = (uint32_t)(j * 64 + lane);
+        ok[j] = col < a.nblk;
+        coff[j] = (ok[j] ? col : 0u) * 20u;
+    }
+    // half h of tile t: rows t*32 + roff + 4h .. +3 of this wave's segment
+    auto load_half = [&](uint32_t t, int h, uint4 (&q)[RH][J], float (&s)[RH][J]) {
+#pragma unroll
+        for (int r = 0; r < RH; ++r) {
+            const uint32_t row = t * 32u + roff + (uint32_t)(RH * h + r);
+            const int nrec = (t < ntiles && row < M) ? (int)row_bytes : 0;
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(wseg + (size_t)row * row_bytes), 0, nrec, kBufFlagsF);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const v4u32f v = __builtin_amdgcn_raw_buffer_load_b128(rs, coff[j], 0, 0);
+                q[r][j] = make_uint4(v[0], v[1], v[2], v[3]);
+                s[r][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, coff[j] + 16u, 0, 0));
+            }
+        }
+    };
+    // Both halves of the first tile are requested before the input digits
+    // and the norm sums (which the first wait then covers as well); from then
+    // on a whole tile is in flight while the current one is computed.
+    uint4 qa[RH][J], qb[RH][J];
+    float sa[RH][J], sb[RH][J];
+    const uint32_t stride = gridDim.x;
+    uint32_t t = blockIdx.x;
+    load_half(t, 0, qa, sa);
+    load_half(t, 1, qb, sb);
+    uint4 xp[J][6];
+    int kk[J];
+    float zz[J];
+    {
+        uint32_t cols[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) cols[j] = coff[j] / 20u;
+        load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
+    }
+    const float rs_norm = norm_scale(a.in_part, a.nblk, a.eps);
+    auto dot_half = [&](const uint4 (&q)[RH][J], const float (&s)[RH][J], float (&out)[RH]) {
+        float acc[RH];
+#pragma unroll
+        for (int r = 0; r < RH; ++r) acc[r] = 0.0f;
+        dot_batch<RH, J>(q, s, xp, kk, zz, ok, acc);
+#pragma unroll
+        for (int r = 0; r < RH; ++r) {
+            float v = acc[r];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            out[r] = v;
+        }
+    };
+    auto epilogue = [&](uint32_t t, const float (&v0)[RH], const float (&v1)[RH]) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < RH; ++r) {
+                red[rg * 8 + r] = v0[r];
+                red[rg * 8 + RH + r] = v1[r];
+            }
+        }
+        __syncthreads();
+        if (rg == 0) {
+            const float gu = rs_norm * red[lane];  // lanes 0..31 gate rows, 32..63 up rows
+            const float up = __shfl(gu, (lane & 31) + 32);
+            const float hv = silu_approx(gu) * up;
+            const bool mine = lane < 32 && t * 32u + (uint32_t)lane < M;
+            prep_lane(mine ? hv : 0.0f, t, lane < 32, a.pad_out, reinterpret_cast<uint32_t*>(a.xd_out));
+        }
+        __syncthreads();  // red[] is reused by the next tile
+    };
+
+    while (t < ntiles) {
+        float v0[RH], v1[RH];
+        dot_half(qa, sa, v0);
+        const uint32_t tn = t + stride;
+        load_half(tn, 0, qa, sa);
+        __builtin_amdgcn_sched_barrier(0);
+        dot_half(qb, sb, v1);
+        load_half(tn, 1, qb, sb);
+        __builtin_amdgcn_sched_barrier(0);
+        epilogue(t, v0, v1);
+        t = tn;
+    }
+}
+
 template <int W, int RG, int RT, int J, int MODE>
 static hipError_t run_fused(const FusedArgs& a, uint32_t tiles, hipStream_t s) {
     if (tiles == 0) return hipSuccess;
@@ -255,11 +355,32 @@ hipError_t launch_fused_resid(FusedArgs a, hipStream_t s) {
     return dispatch<kModeResid>(a, fill_tiles(a), s);
 }
 
+template <int J>
+static hipError_t run_swiglu_p(const FusedArgs& a, uint32_t ntiles, hipStream_t s) {
+    static int occ = 0;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_swiglu_p<J>, 512, 0) != hipSuccess || o < 1) o = 1;
+        occ = o;
+    }
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu < 1)
+        ncu = 256;
+    const uint32_t resident = (uint32_t)(occ * ncu);
+    const uint32_t grid = ntiles < resident ? ntiles : resident;
+    hipLaunchKernelGGL((k_swiglu_p<J>), dim3(grid), dim3(512), 0, s, a, ntiles);
+    return hipGetLastError();
+}
+
 hipError_t launch_fused_swiglu(FusedArgs a, hipStream_t s) {
     a.nseg = 2;
-    if (a.M[0] != a.M[1] || a.M[0] % 32 != 0 || !a.xd_out) return hipErrorInvalidValue;
-    if (a.nblk > 128) return hipErrorInvalidValue;
-    return dispatch<kModeSwiglu>(a, a.M[0] / 32u, s);
+    if (a.M[0] != a.M[1] || a.M[0] % 32 != 0 || !a.xd_out || !a.in_part) return hipErrorInvalidValue;
+    const uint32_t ntiles = a.M[0] / 32u;
+    if (ntiles == 0) return hipSuccess;
+    if (a.nblk <= 64) return run_swiglu_p<1>(a, ntiles, s);
+    if (a.nblk <= 128) return run_swiglu_p<2>(a, ntiles, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_fused_logits(FusedArgs a, hipStream_t s) {

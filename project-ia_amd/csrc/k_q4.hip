@@ -150,6 +150,8 @@ struct GemvArgs {
     const uint32_t* pos;
     const float* cos_tab;
     const float* sin_tab;
+    const float* in_part;  // optional: per-block sums of squares of the un-normalized input
+    float eps;             // (row values are then scaled by the RMSNorm factor)
 };
 
 // Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
@@ -163,6 +165,21 @@ __device__ __forceinline__ void seg_of(const GemvArgs& a, uint32_t t, uint32_t& 
             ++sg;
         }
     }
+}
+
+// RMSNorm factor r = newton(rsqrt(sum/N + eps)) (reference rmsnorm.c:62-71)
+// from per-block sums of squares: each lane sums a strided subset in order,
+// then a butterfly, so every lane of every wave gets the same value.
+__device__ __forceinline__ float gemv_norm_scale(const float* __restrict__ part, uint32_t nblk, float eps) {
+    const int lane = threadIdx.x & 63;
+    float sum = 0.0f;
+    for (uint32_t i = lane; i < nblk; i += 64) sum = sum + part[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / (float)(nblk * 32u);
+    const float av = mean + eps;
+    const float r0 = __builtin_amdgcn_rsqf(av);
+    return (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
 }
 
 // Raw buffer resource word 3 for gfx9-family parts (32-bit untyped data, no
@@ -215,26 +232,23 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     const uint32_t total = a.tile_end[a.nseg - 1];
     const uint32_t stride = gridDim.x * G;
     const uint32_t pos = a.pos ? __builtin_amdgcn_readfirstlane(*a.pos) : 0u;
+    const float rs_norm = a.in_part ? gemv_norm_scale(a.in_part, a.nblk, a.eps) : 1.0f;
 
     uint32_t coff[J];
     bool ok[J];
     uint4 xp[J][6];
     int kk[J];
     float zz[J];
+    {
+        uint32_t cols[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
-        ok[j] = col < a.nblk;
-        const uint32_t cc = ok[j] ? col : 0u;
-        coff[j] = cc * 20u;
-#pragma unroll
-        for (int p = 0; p < 6; ++p) {
-            const uint4 v = a.xd[(size_t)p * a.pad + cc];
-            xp[j][p] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
+        for (int j = 0; j < J; ++j) {
+            const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
+            ok[j] = col < a.nblk;
+            cols[j] = ok[j] ? col : 0u;
+            coff[j] = cols[j] * 20u;
         }
-        const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
-        kk[j] = ok[j] ? (int)meta.x : 0;
-        zz[j] = ok[j] ? __uint_as_float(meta.y) : 0.0f;
+        load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
     }
 
     // Row r of a tile is read through a buffer resource whose base is the
@@ -295,7 +309,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             float v = acc[r];
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            acc[r] = v;
+            acc[r] = v * rs_norm;
         }
         uint32_t sg, tbase;
         seg_of(a, u, sg, tbase);
@@ -557,6 +571,7 @@ static hipError_t run_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const u
         a.pos = dec->pos;
         a.cos_tab = dec->cos_tab;
         a.sin_tab = dec->sin_tab;
+        if (dec->in_part) return hipErrorInvalidValue;  // norm scale: persistent kernel only
     }
     if (tiles == 0) return hipSuccess;
     hipLaunchKernelGGL((k_gemv<W, J, G, RW, R>), dim3(tiles), dim3(64 * W * G), 0, s, a);
@@ -605,6 +620,8 @@ static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const
         a.pos = dec->pos;
         a.cos_tab = dec->cos_tab;
         a.sin_tab = dec->sin_tab;
+        a.in_part = dec->in_part;
+        a.eps = dec->eps;
     }
     if (tiles == 0) return hipSuccess;
     static int occ = 0;

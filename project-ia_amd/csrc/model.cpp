@@ -231,16 +231,12 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
         fd.out_part = p->part_a;
         QH_E(launch_fused_resid(fd, s));
     }
-    FusedArgs fl;
-    fl.w[0] = p->lm_head;
-    fl.M[0] = c.vocab_size;
-    fl.nblk = nblk_d;
-    fl.pad = xd_pad(nblk_d);
-    fl.xd = p->xd_a;
-    fl.in_part = p->part_a;
-    fl.eps = c.rms_norm_eps;
-    fl.y[0] = p->logits;
-    QH_E(launch_fused_logits(fl, s));
+    // LM head on the persistent GEMV with the final RMSNorm factor applied.
+    GemvDecode dn;
+    dn.in_part = p->part_a;
+    dn.eps = c.rms_norm_eps;
+    GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
+    QH_E(launch_gemv(&lm, 1, nblk_d, p->xd_a, s, &dn));
     if (feedback)
         QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->amax_ws, s));
 #undef QH_E

@@ -107,4 +107,29 @@ __device__ __forceinline__ void dot_batch(const uint4 (&q)[R][J], const float (&
         }
 }
 
+// Loads a lane's digit planes and (k, z) for J block columns: column j is
+// cols[j] when ok[j], else it reads zeros.  Buffer loads with an offset past
+// the resource's size return zero, so the loads stay unconditional (no
+// branch, no extra wait) whatever the column mask.
+template <int J>
+__device__ __forceinline__ void load_digits(const uint4* xd, uint32_t pad, const uint32_t (&cols)[J],
+                                            const bool (&ok)[J], uint4 (&xp)[J][6], int (&kk)[J],
+                                            float (&zz)[J]) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xd, 0, (int)(7u * pad * 16u), 0x00020000);
+    const uint32_t kOut = 0x7FFFFFF0u;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+        for (int p = 0; p < 6; ++p) {
+            const v4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ok[j] ? ((uint32_t)p * pad + cols[j]) * 16u : kOut, 0, 0);
+            xp[j][p] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        const v4 m = __builtin_amdgcn_raw_buffer_load_b128(rs, ok[j] ? (6u * pad + cols[j]) * 16u : kOut, 0, 0);
+        kk[j] = (int)m[0];
+        zz[j] = __uint_as_float(m[1]);
+    }
+}
+
 }  // namespace qh

@@ -49,6 +49,11 @@ struct GemvDecode {
     const uint32_t* pos = nullptr;  // current position (device)
     const float* cos_tab = nullptr; // [max_seq][hd] duplicated-pair tables
     const float* sin_tab = nullptr;
+    // Optional RMSNorm factor: when in_part is set (per-block sums of squares
+    // of the un-normalized input whose digits are given), every row value is
+    // multiplied by newton(rsqrt(sum/N + eps)) before the epilogue.
+    const float* in_part = nullptr;
+    float eps = 0.0f;
 };
 
 // y = W . x for up to 4 segments sharing the same x (digit planes xd).
