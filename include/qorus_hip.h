@@ -64,7 +64,9 @@ q_error_code qh_graph_destroy(qh_graph g);
  * reference src/ops/avx2/dequantize.c:18-73).  out must be 16-byte aligned. */
 q_error_code qh_dequantize_q4_0(const void* blocks, float* out, uint64_t n_blocks, qh_stream s);
 
-/* Bytes of workspace qh_gemv_q4_f32 needs for an input of length N. */
+/* Bytes of workspace qh_gemv_q4_f32 may use for an input of length N (it
+ * only touches it when N > 16384; narrower inputs are converted inside the
+ * GEMV launch). */
 size_t qh_gemv_workspace_bytes(uint32_t N);
 
 /* y[M] = W[M x N] . x[N], W->data in HBM (AoS 20-byte Q4_0 blocks, 4-byte
@@ -93,6 +95,18 @@ q_error_code qh_gemv_prepare(const float* x, uint32_t N, void* workspace, qh_str
 q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* const* residuals,
                                      float* const* ys, uint32_t n, const void* workspace,
                                      qh_stream s);
+
+/* ys[i] = Ws[i] . x (+ residuals[i]) for 1 <= n <= 4 matrices with the same
+ * N, straight from the fp32 x: one launch for N <= 16384 (the digit planes
+ * are made inside the GEMV), prepare + GEMV above that (`workspace` as in
+ * qh_gemv_q4_f32, NULL for the library-owned buffer).  Each Ws[i], x and
+ * ys[i] are validated as in qh_gemv_q4_f32; ys[i] must not overlap x.
+ * Results are bit-identical to qh_gemv_prepare + qh_gemv_q4_f32_prepared.
+ * No reference counterpart (the reference calls q_gemv_q4_f32_avx2 once per
+ * matrix, src/models/model.c:1120-1165). */
+q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const* residuals,
+                                  float* const* ys, uint32_t n, const float* x, void* workspace,
+                                  qh_stream s);
 
 /* ---- Batched prefill GEMM (MFMA) ----
  * Y[t][m] = sum_k W[m][k] * X[t][k] for t < T: the prefill projections of

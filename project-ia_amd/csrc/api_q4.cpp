@@ -60,12 +60,13 @@ static q_error_code default_workspace(size_t bytes, void** out) {
 static q_error_code gemv_device(const q_tensor* W, const void* wdev, const float* x, const float* res,
                                 float* y, void* ws, hipStream_t s) {
     const uint32_t M = W->ne[0], N = W->ne[1];
-    uint4* xd = static_cast<uint4*>(ws);
-    QH_TRY(launch_xprep(x, N, nullptr, 0.0f, nullptr, xd, s));
     GemvSeg seg{static_cast<const uint8_t*>(wdev), y, res, M};
-    QH_TRY(launch_gemv(&seg, 1, N / 32, xd, s));
+    QH_TRY(launch_gemv_f32(&seg, 1, N, x, static_cast<uint4*>(ws), s));
     return Q_OK;
 }
+
+// Workspace is only used by inputs wider than the in-kernel conversion.
+static bool needs_workspace(uint32_t N) { return N / 32 > kGemvF32MaxBlk; }
 
 }  // namespace qh
 
@@ -88,7 +89,8 @@ q_error_code qh_gemv_q4_f32(const q_tensor* W, const float* x, float* y, void* w
     QH_TRY_CODE(validate_gemv(W, x, y));
     Device* d;
     QH_TRY_CODE(device(&d));
-    if (!workspace) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    if (!workspace && needs_workspace(W->ne[1]))
+        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
     return gemv_device(W, W->data, x, nullptr, y, workspace, (hipStream_t)s);
 }
 
@@ -98,7 +100,8 @@ q_error_code qh_gemv_q4_f32_add(const q_tensor* W, const float* x, const float* 
     if (!residual) return Q_ERR_INVALID_ARG;
     Device* d;
     QH_TRY_CODE(device(&d));
-    if (!workspace) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    if (!workspace && needs_workspace(W->ne[1]))
+        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
     return gemv_device(W, W->data, x, residual, y, workspace, (hipStream_t)s);
 }
 
@@ -133,6 +136,26 @@ q_error_code qh_gemv_q4_f32_prepared(const q_tensor* const* Ws, const float* con
     Device* d;
     QH_TRY_CODE(device(&d));
     QH_TRY(launch_gemv(segs, (int)n, Ws[0]->ne[1] / 32, static_cast<const uint4*>(workspace), (hipStream_t)s));
+    return Q_OK;
+}
+
+q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const* residuals, float* const* ys,
+                                  uint32_t n, const float* x, void* workspace, qh_stream s) {
+    if (!Ws || !ys || !x) return Q_ERR_INVALID_ARG;
+    if (n < 1 || n > 4) return Q_ERR_INVALID_SIZE;
+    GemvSeg segs[4];
+    for (uint32_t i = 0; i < n; ++i) {
+        const q_tensor* W = Ws[i];
+        if (!W) return Q_ERR_INVALID_ARG;
+        QH_TRY_CODE(validate_gemv(W, x, ys[i]));
+        if (W->ne[1] != Ws[0]->ne[1]) return Q_ERR_INVALID_SIZE;
+        segs[i] = GemvSeg{static_cast<const uint8_t*>(W->data), ys[i], residuals ? residuals[i] : nullptr, W->ne[0]};
+    }
+    const uint32_t N = Ws[0]->ne[1];
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    if (!workspace && needs_workspace(N)) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(N), &workspace));
+    QH_TRY(launch_gemv_f32(segs, (int)n, N, x, static_cast<uint4*>(workspace), (hipStream_t)s));
     return Q_OK;
 }
 
@@ -222,8 +245,8 @@ q_error_code q_gemv_q4_f32_avx2(const q_tensor* __restrict__ weights, const floa
     QH_TRY_CODE(stage(d, 1, xb + (size_t)M * 4, &vbuf));
     float* dx = static_cast<float*>(vbuf);
     float* dy = reinterpret_cast<float*>(static_cast<uint8_t*>(vbuf) + xb);
-    void* ws;
-    QH_TRY_CODE(stage(d, 2, qh_gemv_workspace_bytes(N), &ws));
+    void* ws = nullptr;
+    if (needs_workspace(N)) QH_TRY_CODE(stage(d, 2, qh_gemv_workspace_bytes(N), &ws));
     QH_TRY(hipMemcpyAsync(dx, input, (size_t)N * 4, hipMemcpyHostToDevice, s));
     QH_TRY_CODE(gemv_device(weights, wdev, dx, nullptr, dy, ws, s));
     QH_TRY(hipMemcpyAsync(output, dy, (size_t)M * 4, hipMemcpyDeviceToHost, s));

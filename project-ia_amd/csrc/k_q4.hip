@@ -152,6 +152,7 @@ struct GemvArgs {
     const float* sin_tab;
     const float* in_part;  // optional: per-block sums of squares of the un-normalized input
     float eps;             // (row values are then scaled by the RMSNorm factor)
+    const float* xf;       // fp32 input (N = 32*nblk) when the kernel makes the digits itself
 };
 
 // Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
@@ -218,7 +219,7 @@ __device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, ui
 // the whole workgroup on one tile).  The grid is sized to what stays
 // resident, so there is one wave of workgroups and no per-tile prologue.
 // ---------------------------------------------------------------------------
-template <int W, int J, int G, int RT>
+template <int W, int J, int G, int RT, bool XF>
 __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     static_assert(W == 1 || G == 1, "multi-wave K split runs one tile per workgroup");
     const int lane = threadIdx.x & 63;
@@ -239,17 +240,82 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     uint4 xp[J][6];
     int kk[J];
     float zz[J];
-    {
-        uint32_t cols[J];
+    uint32_t cols[J];
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
-            ok[j] = col < a.nblk;
-            cols[j] = ok[j] ? col : 0u;
-            coff[j] = cols[j] * 20u;
-        }
+    for (int j = 0; j < J; ++j) {
+        const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
+        ok[j] = col < a.nblk;
+        cols[j] = ok[j] ? col : 0u;
+        coff[j] = cols[j] * 20u;
+    }
+    // fp32 input: x is loaded with coalesced 16-byte loads before the first
+    // tiles' weight loads (so the conversion waits for x only), staged in
+    // LDS at a 36-float stride per block (conflict-free 16-byte reads), and
+    // thread t then converts blocks t, t + 64*W*G, ... into digit planes in
+    // the same LDS space.
+    constexpr int kMaxBlk = 64 * J * W;
+    constexpr int kThreads = 64 * W * G;
+    constexpr int kPass = XF ? (kMaxBlk + kThreads - 1) / kThreads : 0;
+    constexpr int kLd = XF ? (kMaxBlk * 8 + kThreads - 1) / kThreads : 0;
+    constexpr int kXs = 36;
+    constexpr int kLds = !XF ? 1 : (kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
+    __shared__ uint4 lds[kLds];
+    v4u32 xl[kLd > 0 ? kLd : 1];
+    if constexpr (XF) {
+        const __amdgpu_buffer_rsrc_t rx =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.xf, 0, (int)(a.nblk * 128u), kBufFlags);
+#pragma unroll
+        for (int i = 0; i < kLd; ++i)
+            xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)(i * kThreads) + threadIdx.x) * 16u, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
         load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
     }
+    // x staged, converted, and the digits of this lane's columns loaded.
+    auto convert_x = [&]() {
+        float* xs = reinterpret_cast<float*>(lds);
+#pragma unroll
+        for (int i = 0; i < kLd; ++i) {
+            const uint32_t f = (uint32_t)(i * kThreads) + threadIdx.x;
+            if (f < (uint32_t)kMaxBlk * 8u)
+                *reinterpret_cast<v4u32*>(xs + (f >> 3) * kXs + (f & 7u) * 4u) = xl[i];
+        }
+        __syncthreads();
+        float xv[kPass > 0 ? kPass : 1][32];
+#pragma unroll
+        for (int ps = 0; ps < kPass; ++ps) {
+            const uint32_t c = (uint32_t)(ps * kThreads) + threadIdx.x;
+            const uint32_t cc = c < (uint32_t)kMaxBlk ? c : 0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const v4u32 v = *reinterpret_cast<const v4u32*>(xs + cc * kXs + (uint32_t)i * 4u);
+                xv[ps][4 * i] = __uint_as_float(v[0]);
+                xv[ps][4 * i + 1] = __uint_as_float(v[1]);
+                xv[ps][4 * i + 2] = __uint_as_float(v[2]);
+                xv[ps][4 * i + 3] = __uint_as_float(v[3]);
+            }
+        }
+        __syncthreads();  // the planes overwrite the staged x
+#pragma unroll
+        for (int ps = 0; ps < kPass; ++ps) {
+            const uint32_t c = (uint32_t)(ps * kThreads) + threadIdx.x;
+            if (c < (uint32_t)kMaxBlk) {
+                uint4 o[7];
+                prep_block(xv[ps], o);
+#pragma unroll
+                for (int p = 0; p < 7; ++p) lds[p * kMaxBlk + c] = o[p];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+#pragma unroll
+            for (int p = 0; p < 6; ++p) xp[j][p] = lds[p * kMaxBlk + cols[j]];
+            const uint4 m = lds[6 * kMaxBlk + cols[j]];
+            kk[j] = ok[j] ? (int)m.x : 0;
+            zz[j] = ok[j] ? __uint_as_float(m.y) : 0.0f;
+        }
+    };
 
     // Row r of a tile is read through a buffer resource whose base is the
     // row and whose size is the row's bytes (0 past the last row): the
@@ -346,6 +412,10 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     Epi ea, eb;
     uint32_t u = blockIdx.x * G + g;
     load_tile(u, qa, sa, ea);
+    if constexpr (XF) {
+        __builtin_amdgcn_sched_barrier(0);
+        convert_x();
+    }
     // The scheduling barriers keep the next tile's loads issued before any
     // instruction that waits on the current tile's data.
     while (u < total) {
@@ -591,9 +661,28 @@ static int num_cu() {
     return g_num_cu;
 }
 
+// Persistent grid: as many groups of G tiles as are resident at once.
+template <int W, int J, int G, int RT, bool XF>
+static hipError_t launch_gemv_p(const GemvArgs& a, uint32_t tiles, hipStream_t s) {
+    static int occ = 0;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT, XF>, 64 * W * G, 0) != hipSuccess ||
+            o < 1)
+            o = 1;
+        occ = o;
+    }
+    const uint32_t groups = (tiles + G - 1) / G;
+    const uint32_t resident = (uint32_t)(occ * num_cu());
+    const uint32_t grid = groups < resident ? groups : resident;
+    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT, XF>), dim3(grid), dim3(64 * W * G), 0, s, a);
+    return hipGetLastError();
+}
+
+// xd: prepared digit planes, or xf: the fp32 input (converted in-kernel).
 template <int W, int J, int G, int RT>
-static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
-                             const GemvDecode* dec) {
+static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, const float* xf,
+                             hipStream_t s, const GemvDecode* dec) {
     GemvArgs a{};
     uint32_t tiles = 0;
     for (int i = 0; i < 4; ++i) {
@@ -623,19 +712,10 @@ static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const
         a.in_part = dec->in_part;
         a.eps = dec->eps;
     }
+    a.xf = xf;
     if (tiles == 0) return hipSuccess;
-    static int occ = 0;
-    if (occ == 0) {
-        int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT>, 64 * W * G, 0) != hipSuccess || o < 1)
-            o = 1;
-        occ = o;
-    }
-    const uint32_t groups = (tiles + G - 1) / G;
-    const uint32_t resident = (uint32_t)(occ * num_cu());
-    const uint32_t grid = groups < resident ? groups : resident;
-    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT>), dim3(grid), dim3(64 * W * G), 0, s, a);
-    return hipGetLastError();
+    if (xf) return launch_gemv_p<W, J, G, RT, true>(a, tiles, s);
+    return launch_gemv_p<W, J, G, RT, false>(a, tiles, s);
 }
 
 // Launch shape by input width (nblk = N/32 blocks).  Inputs that fit one
@@ -643,12 +723,28 @@ static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const
 hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd, hipStream_t s,
                        const GemvDecode* dec) {
     if (nseg < 1 || nseg > 4) return hipErrorInvalidValue;
-    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, xd, s, dec);
-    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, xd, s, dec);
+    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
+    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
+    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
+    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
+    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
     return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
+}
+
+// fp32 input: inputs of up to kGemvF32MaxBlk blocks are converted inside the
+// GEMV (one launch); wider ones go through k_xprep into ws first.
+hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws, hipStream_t s) {
+    if (nseg < 1 || nseg > 4 || N == 0 || N % 32 != 0) return hipErrorInvalidValue;
+    const uint32_t nblk = N / 32;
+    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
+    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
+    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
+    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, nullptr);
+    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, nullptr);
+    if (!ws) return hipErrorInvalidValue;
+    hipError_t e = launch_xprep(x, N, nullptr, 0.0f, nullptr, ws, s);
+    if (e != hipSuccess) return e;
+    return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, ws, s, nullptr);
 }
 
 }  // namespace qh

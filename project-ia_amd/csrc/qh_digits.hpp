@@ -64,6 +64,64 @@ __device__ inline void prep_lane(float v, uint32_t c, bool store, uint32_t pad, 
     }
 }
 
+// One thread converts one whole 32-element block v[0..32) into the digit
+// planes prep_lane produces for it: out[0..5] = planes 0..5 (dword i holds
+// elements 8i..8i+7, already XORed with 0x88888888), out[6] = (k, z, 0, 0).
+// The block maximum is an unsigned maximum over the bit patterns shifted
+// left by one (the sign dropped), which also flags infinities and NaNs
+// (pattern >= 0xFF000000).  Such a block gets z = NaN; its digits are then
+// those of the zero block.  The nibble transpose works on element pairs
+// (u0, u1): lo = nibbles 0, 2, 4 of u0 in the low and of u1 in the high
+// half of bytes 0..2, hi = nibbles 1, 3, 5 likewise; byte b of the four
+// pairs' words of 8 elements is plane 2b (lo) or 2b+1 (hi), gathered with
+// byte permutes.
+__device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[7]) {
+    uint32_t mb = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) mb = __builtin_elementwise_max(mb, __float_as_uint(v[e]) << 1);
+    const bool bad = mb >= 0xFF000000u;
+    const float m = __uint_as_float(mb >> 1);
+    int k = 0;
+    if (!bad && m > 0.0f) {
+        const int E = __builtin_amdgcn_frexp_expf(m);  // m < 2^E
+        k = 23 - E;
+        if (rintf(ldexpf(m, k)) > (float)kDigitMax) k -= 1;
+    }
+    uint32_t pl[6][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+            const float a0 = bad ? 0.0f : v[8 * i + 2 * pr], a1 = bad ? 0.0f : v[8 * i + 2 * pr + 1];
+            const uint32_t u0 = (uint32_t)((int)rintf(ldexpf(a0, k)) + (int)kDigitBias);
+            const uint32_t u1 = (uint32_t)((int)rintf(ldexpf(a1, k)) + (int)kDigitBias);
+            lo[pr] = (u0 & 0x0F0F0F0Fu) | ((u1 << 4) & 0xF0F0F0F0u);
+            hi[pr] = ((u0 >> 4) & 0x0F0F0F0Fu) | (u1 & 0xF0F0F0F0u);
+        }
+        // t = (w0.b0, w1.b0, w0.b1, w1.b1), s = (w0.b2, w1.b2, -, -)
+        const uint32_t tl01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x05010400u);
+        const uint32_t tl23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x05010400u);
+        const uint32_t sl01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x00000602u);
+        const uint32_t sl23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x00000602u);
+        const uint32_t th01 = __builtin_amdgcn_perm(hi[1], hi[0], 0x05010400u);
+        const uint32_t th23 = __builtin_amdgcn_perm(hi[3], hi[2], 0x05010400u);
+        const uint32_t sh01 = __builtin_amdgcn_perm(hi[1], hi[0], 0x00000602u);
+        const uint32_t sh23 = __builtin_amdgcn_perm(hi[3], hi[2], 0x00000602u);
+        pl[0][i] = __builtin_amdgcn_perm(tl23, tl01, 0x05040100u);
+        pl[2][i] = __builtin_amdgcn_perm(tl23, tl01, 0x07060302u);
+        pl[4][i] = __builtin_amdgcn_perm(sl23, sl01, 0x05040100u);
+        pl[1][i] = __builtin_amdgcn_perm(th23, th01, 0x05040100u);
+        pl[3][i] = __builtin_amdgcn_perm(th23, th01, 0x07060302u);
+        pl[5][i] = __builtin_amdgcn_perm(sh23, sh01, 0x05040100u);
+    }
+#pragma unroll
+    for (int p = 0; p < 6; ++p)
+        out[p] = make_uint4(pl[p][0] ^ 0x88888888u, pl[p][1] ^ 0x88888888u, pl[p][2] ^ 0x88888888u,
+                            pl[p][3] ^ 0x88888888u);
+    out[6] = make_uint4((uint32_t)k, __float_as_uint(bad ? __builtin_nanf("") : 0.0f), 0u, 0u);
+}
+
 // Integer dots of R*J blocks (already loaded) against the x digit planes,
 // accumulated into acc[0..R): plane by plane across all blocks, each plane a
 // 4-deep dot8 chain of its own, planes combined by P = (P << 4) + S_p, so

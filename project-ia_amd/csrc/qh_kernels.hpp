@@ -59,6 +59,12 @@ struct GemvDecode {
 // y = W . x for up to 4 segments sharing the same x (digit planes xd).
 hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4* xd,
                        hipStream_t s, const GemvDecode* dec = nullptr);
+// Same from the fp32 input x[N]: inputs of up to kGemvF32MaxBlk 32-element
+// blocks are converted to digit planes inside the GEMV launch; wider ones
+// are prepared into ws (xd_bytes(N/32) bytes) by a separate launch first.
+constexpr uint32_t kGemvF32MaxBlk = 512;
+hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws,
+                           hipStream_t s);
 
 // ---- batched prefill GEMM (k_gemm.hip) ----
 // Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 or 2) matrices sharing

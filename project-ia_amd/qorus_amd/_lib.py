@@ -143,6 +143,7 @@ def lib():
     _sig(L, "qh_gemv_q4_f32_add", i32, vp, vp, vp, vp, vp, vp)
     _sig(L, "qh_gemv_prepare", i32, vp, u32, vp, vp)
     _sig(L, "qh_gemv_q4_f32_prepared", i32, vp, vp, vp, u32, vp, vp)
+    _sig(L, "qh_gemv_q4_f32_multi", i32, vp, vp, vp, u32, vp, vp, vp)
     _sig(L, "qh_gemm_workspace_bytes", C.c_size_t, u32, u32, u32)
     _sig(L, "qh_gemm_q4_f32", i32, vp, vp, u32, vp, vp, vp)
     _sig(L, "qh_gemm_q4_f32_multi", i32, vp, vp, u32, vp, u32, vp, vp)

@@ -240,3 +240,64 @@ def test_gemv_tiny_and_mixed_magnitude_inputs(qa):
               np.where(rng.random(N) < 0.05, 1e6, 1e-6).astype(np.float32) * orc.gen_f32(N, rng)):
         y64, cond = orc.gemv_f64(W, M, N, x)
         assert stats(g(x), y64, cond)[0] <= 1e-5
+
+
+# Input widths around every launch-shape boundary of the fp32-input GEMV
+# (in-kernel digit conversion up to 512 blocks, prepare + GEMV above).
+F32_WIDTHS = [32, 2048, 2080, 4096, 4128, 8192, 8224, 14336, 14368, 16384, 16416]
+
+
+def special_input(N, rng):
+    """N(0,1) with whole blocks of zeros, subnormals, huge values and a
+    block mixing magnitudes 2^-60..2^60."""
+    x = orc.gen_f32(N, rng)
+    nb = N // 32
+    if nb >= 4:
+        x[0:32] = 0.0
+        x[32:64] = rng.standard_normal(32).astype(np.float32) * np.float32(1e-40)
+        x[64:96] = rng.standard_normal(32).astype(np.float32) * np.float32(3e37)
+        x[96:128] = (rng.standard_normal(32) * 2.0 ** rng.integers(-60, 60, 32)).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("N", F32_WIDTHS)
+def test_gemv_f32_multi_bitexact_vs_prepared(qa, N):
+    """qh_gemv_q4_f32_multi (digit planes made inside the GEMV) must equal
+    qh_gemv_prepare + qh_gemv_q4_f32_prepared bit for bit, with 1-3
+    matrices, residuals, and NaN/Inf blocks (non-finite rows match too)."""
+    lib = qa.lib()
+    rng = orc.rng_for(109, N)
+    Ms = [37, 8, 130][: 1 + (N // 32) % 3]
+    Ws = [orc.gen_q4(M, N, rng) for M in Ms]
+    dW = [qa.DeviceBuffer.from_numpy(np.ascontiguousarray(W)) for W in Ws]
+    ts = [qa.q4_tensor(d.ptr, M, N) for d, M in zip(dW, Ms)]
+    tp = (C.c_void_p * len(ts))(*[t.addr for t in ts])
+    dx = qa.DeviceBuffer(N * 4)
+    ya = [qa.DeviceBuffer(M * 4) for M in Ms]
+    yb = [qa.DeviceBuffer(M * 4) for M in Ms]
+    rs = [qa.DeviceBuffer.from_numpy(orc.gen_f32(M, rng)) for M in Ms]
+    ws = qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(N))
+    yap = (C.c_void_p * len(Ms))(*[b.ptr for b in ya])
+    ybp = (C.c_void_p * len(Ms))(*[b.ptr for b in yb])
+    rsp = (C.c_void_p * len(Ms))(*[b.ptr for b in rs])
+    inputs = [orc.gen_f32(N, rng), special_input(N, rng)]
+    if N >= 256:
+        bad = special_input(N, rng)
+        bad[160 + 5] = np.nan
+        bad[192 + 31] = np.inf
+        inputs.append(bad)
+    for x in inputs:
+        for res in (None, rsp):
+            dx.upload(x)
+            qa.check(lib.qh_gemv_q4_f32_multi(tp, res, yap, len(Ms), dx.ptr, None, None), "multi")
+            qa.check(lib.qh_gemv_prepare(dx.ptr, N, ws.ptr, None), "prepare")
+            qa.check(lib.qh_gemv_q4_f32_prepared(tp, res, ybp, len(Ms), ws.ptr, None), "prepared")
+            qa.check(lib.qh_device_synchronize(), "sync")
+            for a, b, M in zip(ya, yb, Ms):
+                assert same_bits_nan(a.download(np.float32, (M,)), b.download(np.float32, (M,))), (N, M)
+    # Accuracy of the one-launch path itself.
+    y64, cond = orc.gemv_f64(Ws[0], Ms[0], N, inputs[0])
+    dx.upload(inputs[0])
+    qa.check(lib.qh_gemv_q4_f32_multi(tp, None, yap, len(Ms), dx.ptr, None, None), "multi")
+    qa.check(lib.qh_device_synchronize(), "sync")
+    assert stats(ya[0].download(np.float32, (Ms[0],)), y64, cond)[0] <= 1e-5
