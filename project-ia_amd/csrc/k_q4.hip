@@ -218,6 +218,9 @@ __device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, ui
 // groups (G > 1 only with W == 1: the cross-wave reduction of W > 1 needs
 // the whole workgroup on one tile).  The grid is sized to what stays
 // resident, so there is one wave of workgroups and no per-tile prologue.
+// Each tile step costs about one HBM latency (one tile of prefetch), so a
+// wave's time follows its number of tiles: splitting rows into smaller,
+// evenly balanced pieces adds steps and measured slower.
 // ---------------------------------------------------------------------------
 template <int W, int J, int G, int RT, bool XF>
 __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
@@ -398,10 +401,13 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             __syncthreads();
             if ((int)threadIdx.x < RT) {
                 const int r = threadIdx.x;
-                float v = red[0][r];
+                float v = red[0][r], pv = red[0][r ^ 1];
 #pragma unroll
-                for (int k2 = 1; k2 < W; ++k2) v += red[k2][r];
-                store_row_pre(a, sg, row0 + r, v, 0.0f, false, pos, e.res, e.c, e.sn);
+                for (int k2 = 1; k2 < W; ++k2) {
+                    v += red[k2][r];
+                    pv += red[k2][r ^ 1];
+                }
+                store_row_pre(a, sg, row0 + r, v, pv, r & 1, pos, e.res, e.c, e.sn);
             }
             __syncthreads();  // red[] is reused by the next tile
         }
@@ -417,7 +423,8 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         convert_x();
     }
     // The scheduling barriers keep the next tile's loads issued before any
-    // instruction that waits on the current tile's data.
+    // instruction that waits on the current tile's data.  (Two tiles of
+    // prefetch measured slower: more concurrent row streams.)
     while (u < total) {
         uint32_t un = u + stride;
         load_tile(un, qb, sb, eb);
@@ -695,7 +702,7 @@ static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const
             a.head_stride[i] = segs[i].head_stride;
             a.pos_stride[i] = segs[i].pos_stride;
             if (segs[i].rope) a.rope_mask |= 1u << i;
-            if (segs[i].hd && (W != 1 || !dec || !dec->pos || (segs[i].hd % 2) != 0)) return hipErrorInvalidValue;
+            if (segs[i].hd && (!dec || !dec->pos || (segs[i].hd % 2) != 0)) return hipErrorInvalidValue;
             if (segs[i].rope && (!dec->cos_tab || !dec->sin_tab || (RT % 2) != 0)) return hipErrorInvalidValue;
             tiles += (segs[i].M + RT - 1) / RT;
         }

@@ -372,8 +372,12 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     if (h->n_layers == 0 || h->dim == 0 || h->vocab_size == 0 || h->n_heads == 0 || h->n_kv_heads == 0)
         return Q_ERR_INVALID_CONFIG;
     if (h->dim % 32 != 0 || h->hidden_dim % 32 != 0) return Q_ERR_INVALID_CONFIG;
-    // This build: version-3 layout, GQA group dividing the heads, 128-wide heads.
+    // This build: version-3 layout, GQA group dividing the heads, 128-wide
+    // heads, d_model up to 16384 (the Q|K|V epilogue's persistent GEMV).
     if (h->version < 3 || h->hidden_dim == 0 || h->max_seq_len == 0) return Q_ERR_INVALID_CONFIG;
+    if (h->dim / 32 > kGemvF32MaxBlk) return Q_ERR_INVALID_CONFIG;
+    const uint32_t group = h->n_kv_heads ? h->n_heads / h->n_kv_heads : 0;
+    if (group != 1 && group != 2 && group != 4 && group != 8) return Q_ERR_INVALID_CONFIG;  // GQA groups built
     if (h->n_heads % h->n_kv_heads != 0 || h->dim % h->n_heads != 0 || h->dim / h->n_heads != 128)
         return Q_ERR_INVALID_CONFIG;
     CtxState* st = ctx_state(ctx, false);

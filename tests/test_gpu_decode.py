@@ -138,3 +138,39 @@ def test_model_api_errors(qa, tmp_path):
         assert out.value == 37
     finally:
         m.close()
+
+
+def test_decode_unfused_wide_dim(qa, tmp_path):
+    """d_model 4352 (136 blocks, above the fused kernels' 128): the layer
+    runs on the generic GEMV launches (RMSNorm + digit prep, Q|K|V with RoPE
+    and head-strided cache stores on the two-wave K split, residual
+    epilogues), GQA 34/17."""
+    h = qa.QorusHeader(vocab=300, dim=4352, hidden=1024, n_layers=2, n_heads=34, n_kv=17, max_seq=64)
+    P = 20
+    m, blob, kv = build(qa, tmp_path, h, 15, P, name="wide.qorus")
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        t = 5
+        for pos in range(P, P + 3):
+            tok_ref, lg_ref = ref.step(t, pos)
+            lg = m.forward([t], pos)
+            assert rel_err(lg, lg_ref) <= 1e-4, pos
+            assert int(np.argmax(lg)) == tok_ref
+            t = tok_ref
+        kv_gpu = m.download_kv().reshape(kv.shape)
+        for l in range(h.n_layers):
+            assert rel_err(kv_gpu[l, :, P], ref.kv[l, :, P]) <= 1e-4
+    finally:
+        m.close()
+
+
+def test_build_graph_rejects_unbuilt_configs(qa, tmp_path):
+    """GQA groups other than 1/2/4/8 are refused at llama_build_graph with
+    Q_ERR_INVALID_CONFIG (not at the first step)."""
+    for i, h in enumerate([qa.QorusHeader(vocab=50, dim=384, hidden=256, n_layers=1, n_heads=3, n_kv=1, max_seq=16),
+                           qa.QorusHeader(vocab=50, dim=1536, hidden=256, n_layers=1, n_heads=12, n_kv=2,
+                                          max_seq=16)]):
+        path = tmp_path / f"bad{i}.qorus"
+        qa.synthetic.write_synthetic_model(path, h, 16)
+        with pytest.raises(qa.QorusError, match="INVALID_CONFIG"):
+            qa.Model(path)
