@@ -153,6 +153,7 @@ struct GemvArgs {
     const float* in_part;  // optional: per-block sums of squares of the un-normalized input
     float eps;             // (row values are then scaled by the RMSNorm factor)
     const float* xf;       // fp32 input (N = 32*nblk) when the kernel makes the digits itself
+    const float* xnorm_w;  // with xf: RMSNorm weight; digits of x*w, rows scaled by the norm factor
 };
 
 // Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     const uint32_t total = a.tile_end[a.nseg - 1];
     const uint32_t stride = gridDim.x * G;
     const uint32_t pos = a.pos ? __builtin_amdgcn_readfirstlane(*a.pos) : 0u;
-    const float rs_norm = a.in_part ? gemv_norm_scale(a.in_part, a.nblk, a.eps) : 1.0f;
+    float rs_norm = a.in_part ? gemv_norm_scale(a.in_part, a.nblk, a.eps) : 1.0f;
 
     uint32_t coff[J];
     bool ok[J];
@@ -263,27 +264,64 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     constexpr int kXs = 36;
     constexpr int kLds = !XF ? 1 : (kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
     __shared__ uint4 lds[kLds];
-    v4u32 xl[kLd > 0 ? kLd : 1];
+    __shared__ float lds_ss[XF ? W * G : 1];
+    v4u32 xl[kLd > 0 ? kLd : 1], wl[kLd > 0 ? kLd : 1];
     if constexpr (XF) {
         const __amdgpu_buffer_rsrc_t rx =
             __builtin_amdgcn_make_buffer_rsrc((void*)a.xf, 0, (int)(a.nblk * 128u), kBufFlags);
+        const __amdgpu_buffer_rsrc_t rw =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.xnorm_w, 0, a.xnorm_w ? (int)(a.nblk * 128u) : 0, kBufFlags);
 #pragma unroll
-        for (int i = 0; i < kLd; ++i)
-            xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)(i * kThreads) + threadIdx.x) * 16u, 0, 0);
+        for (int i = 0; i < kLd; ++i) {
+            const uint32_t off = ((uint32_t)(i * kThreads) + threadIdx.x) * 16u;
+            xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+            wl[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
     } else {
         load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
     }
-    // x staged, converted, and the digits of this lane's columns loaded.
+    // x (or x*w with the RMSNorm weight) staged, converted, and the digits
+    // of this lane's columns loaded.  RMSNorm: the sum of x^2 is taken per
+    // thread over its 16-byte pieces in order, per wave by a butterfly, then
+    // over the waves in order, so every wave of every workgroup gets the
+    // same factor newton(rsqrt(sum/N + eps)) (reference rmsnorm.c:62-71).
     auto convert_x = [&]() {
         float* xs = reinterpret_cast<float*>(lds);
+        const bool norm = a.xnorm_w != nullptr;
+        float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < kLd; ++i) {
             const uint32_t f = (uint32_t)(i * kThreads) + threadIdx.x;
-            if (f < (uint32_t)kMaxBlk * 8u)
-                *reinterpret_cast<v4u32*>(xs + (f >> 3) * kXs + (f & 7u) * 4u) = xl[i];
+            v4u32 v = xl[i];
+            float x0 = __uint_as_float(v[0]), x1 = __uint_as_float(v[1]);
+            float x2 = __uint_as_float(v[2]), x3 = __uint_as_float(v[3]);
+            ss = ss + x0 * x0;
+            ss = ss + x1 * x1;
+            ss = ss + x2 * x2;
+            ss = ss + x3 * x3;
+            if (norm) {
+                v[0] = __float_as_uint(x0 * __uint_as_float(wl[i][0]));
+                v[1] = __float_as_uint(x1 * __uint_as_float(wl[i][1]));
+                v[2] = __float_as_uint(x2 * __uint_as_float(wl[i][2]));
+                v[3] = __float_as_uint(x3 * __uint_as_float(wl[i][3]));
+            }
+            if (f < (uint32_t)kMaxBlk * 8u) *reinterpret_cast<v4u32*>(xs + (f >> 3) * kXs + (f & 7u) * 4u) = v;
+        }
+        if (norm) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) lds_ss[wave] = ss;
         }
         __syncthreads();
+        if (norm) {
+            float tot = lds_ss[0];
+#pragma unroll
+            for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
+            const float av = tot / (float)(a.nblk * 32u) + a.eps;
+            const float r0 = __builtin_amdgcn_rsqf(av);
+            rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
+        }
         float xv[kPass > 0 ? kPass : 1][32];
 #pragma unroll
         for (int ps = 0; ps < kPass; ++ps) {
@@ -720,6 +758,7 @@ static hipError_t run_gemv_p(const GemvSeg* segs, int nseg, uint32_t nblk, const
         a.eps = dec->eps;
     }
     a.xf = xf;
+    a.xnorm_w = (xf && dec) ? dec->norm_w : nullptr;
     if (tiles == 0) return hipSuccess;
     if (xf) return launch_gemv_p<W, J, G, RT, true>(a, tiles, s);
     return launch_gemv_p<W, J, G, RT, false>(a, tiles, s);
@@ -740,18 +779,20 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4
 
 // fp32 input: inputs of up to kGemvF32MaxBlk blocks are converted inside the
 // GEMV (one launch); wider ones go through k_xprep into ws first.
-hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws, hipStream_t s) {
+hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws, hipStream_t s,
+                           const GemvDecode* dec) {
     if (nseg < 1 || nseg > 4 || N == 0 || N % 32 != 0) return hipErrorInvalidValue;
+    if (dec && dec->in_part) return hipErrorInvalidValue;
     const uint32_t nblk = N / 32;
-    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
-    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
-    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, nullptr, x, s, nullptr);
-    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, nullptr);
-    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, nullptr);
-    if (!ws) return hipErrorInvalidValue;
+    if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, nullptr, x, s, dec);
+    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, nullptr, x, s, dec);
+    if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, nullptr, x, s, dec);
+    if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, dec);
+    if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, nullptr, x, s, dec);
+    if (!ws || (dec && dec->norm_w)) return hipErrorInvalidValue;
     hipError_t e = launch_xprep(x, N, nullptr, 0.0f, nullptr, ws, s);
     if (e != hipSuccess) return e;
-    return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, ws, s, nullptr);
+    return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, ws, s, dec);
 }
 
 }  // namespace qh

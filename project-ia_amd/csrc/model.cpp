@@ -57,7 +57,7 @@ struct ModelPlan {
     uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
     uint32_t hist_cap = 0;
     float* amax_ws = nullptr;                // multi-workgroup argmax partials
-    float *part_a = nullptr, *part_b = nullptr;  // per-block sums of squares of the RMSNorm inputs
+    float* part_b = nullptr;                 // per-block sums of squares of the FFN RMSNorm input
     bool fused = false;                      // 7-kernel layers (k_fused.hip)
     float* kv = nullptr;
     size_t kv_layer_floats = 0;
@@ -134,9 +134,11 @@ static q_tensor* make_view(q_context* ctx, size_t offset, uint32_t n0, uint32_t 
 // ---------------------------------------------------------------------------
 // Decode step enqueue (all kernels on p->stream)
 // ---------------------------------------------------------------------------
-// One decode step with the fused kernels: per layer QKV(+norm scale, RoPE,
-// KV store), attention (3 kernels), Wo(+residual, next norm's digits),
-// gate|up(+norm scale, SwiGLU, digits), down(+residual, next norm's digits).
+// One decode step with the fused kernels: per layer QKV (RMSNorm and digits
+// in the prologue, RoPE and KV stores in the epilogue), attention (3
+// kernels: the reference's clamped polynomial exp needs the global max
+// before any exponential), Wo (+residual, the FFN norm's digits and block sums), gate|up
+// (+norm scale, SwiGLU, digits), down (+residual).
 static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
     const q_llama_config& c = p->cfg;
     hipStream_t s = p->stream;
@@ -147,35 +149,34 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
         if (e != hipSuccess) return e;   \
     } while (0)
     const uint32_t nblk_d = c.dim / 32, nblk_h = c.hidden_dim / 32;
-    QH_E(launch_embed_prep(p->embd, p->tok, c.vocab_size, c.dim, p->layers[0].attn_norm, p->x, p->xd_a, p->part_a, s));
+    QH_E(launch_embed(p->embd, p->tok, c.vocab_size, c.dim, p->x, s));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const LayerDev& L = p->layers[l];
         float* kvl = p->kv + (size_t)l * p->kv_layer_floats;
-        FusedArgs fq;
-        fq.w[0] = L.wq;
-        fq.w[1] = L.wk;
-        fq.w[2] = L.wv;
-        fq.M[0] = c.dim;
-        fq.M[1] = p->kvd;
-        fq.M[2] = p->kvd;
-        fq.nseg = 3;
-        fq.nblk = nblk_d;
-        fq.pad = xd_pad(nblk_d);
-        fq.xd = p->xd_a;
-        fq.in_part = p->part_a;
-        fq.eps = c.rms_norm_eps;
-        fq.y[0] = p->q;
-        fq.y[1] = kvl;
-        fq.y[2] = kvl + p->hd;
-        for (int i = 0; i < 3; ++i) fq.hd[i] = p->hd;
-        fq.head_stride[0] = p->hd;
-        fq.head_stride[1] = fq.head_stride[2] = c.max_seq_len * 2 * p->hd;
-        fq.pos_stride[1] = fq.pos_stride[2] = 2 * p->hd;
-        fq.rope_mask = 3u;
-        fq.pos = p->pos;
-        fq.cos_tab = p->cos_tab;
-        fq.sin_tab = p->sin_tab;
-        QH_E(launch_fused_qkv(fq, s));
+        // Q|K|V of RMSNorm(x): the norm and the digits of x*attn_norm are
+        // made in the GEMV's prologue; RoPE and the KV-cache stores in its
+        // epilogue.
+        GemvSeg qkv[3];
+        qkv[0] = GemvSeg{L.wq, p->q, nullptr, c.dim};
+        qkv[0].hd = p->hd;
+        qkv[0].head_stride = p->hd;
+        qkv[0].rope = true;
+        qkv[1] = GemvSeg{L.wk, kvl, nullptr, p->kvd};
+        qkv[1].hd = p->hd;
+        qkv[1].head_stride = c.max_seq_len * 2 * p->hd;
+        qkv[1].pos_stride = 2 * p->hd;
+        qkv[1].rope = true;
+        qkv[2] = GemvSeg{L.wv, kvl + p->hd, nullptr, p->kvd};
+        qkv[2].hd = p->hd;
+        qkv[2].head_stride = c.max_seq_len * 2 * p->hd;
+        qkv[2].pos_stride = 2 * p->hd;
+        GemvDecode dq;
+        dq.pos = p->pos;
+        dq.cos_tab = p->cos_tab;
+        dq.sin_tab = p->sin_tab;
+        dq.norm_w = L.attn_norm;
+        dq.eps = c.rms_norm_eps;
+        QH_E(launch_gemv_f32(qkv, 3, c.dim, p->x, nullptr, s, &dq));
         AttnArgs aa;
         aa.q = p->q;
         aa.kv_layer = kvl;
@@ -217,26 +218,15 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
         fg.xd_out = p->xd_c;
         fg.pad_out = xd_pad(nblk_h);
         QH_E(launch_fused_swiglu(fg, s));
-        FusedArgs fd;
-        fd.w[0] = L.wd;
-        fd.M[0] = c.dim;
-        fd.nblk = nblk_h;
-        fd.pad = xd_pad(nblk_h);
-        fd.xd = p->xd_c;
-        fd.y[0] = p->x;
-        fd.res = p->x1;
-        fd.wnorm = (l + 1 < c.n_layers) ? p->layers[l + 1].attn_norm : p->out_norm;
-        fd.xd_out = p->xd_a;
-        fd.pad_out = xd_pad(nblk_d);
-        fd.out_part = p->part_a;
-        QH_E(launch_fused_resid(fd, s));
+        GemvSeg wd{L.wd, p->x, p->x1, c.dim};
+        QH_E(launch_gemv(&wd, 1, nblk_h, p->xd_c, s));
     }
-    // LM head on the persistent GEMV with the final RMSNorm factor applied.
+    // LM head of RMSNorm(x), the norm made in the GEMV's prologue.
     GemvDecode dn;
-    dn.in_part = p->part_a;
+    dn.norm_w = p->out_norm;
     dn.eps = c.rms_norm_eps;
     GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
-    QH_E(launch_gemv(&lm, 1, nblk_d, p->xd_a, s, &dn));
+    QH_E(launch_gemv_f32(&lm, 1, c.dim, p->x, nullptr, s, &dn));
     if (feedback)
         QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->amax_ws, s));
 #undef QH_E
@@ -528,7 +518,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
     const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
     const size_t o_aw = carve(argmax_workspace_bytes(cfg.vocab_size));
-    const size_t o_pa = carve(cfg.dim / 32 * 4), o_pb = carve(cfg.dim / 32 * 4);
+    const size_t o_pb = carve(cfg.dim / 32 * 4);
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
@@ -560,7 +550,6 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
     p->amax_ws = reinterpret_cast<float*>(A + o_aw);
-    p->part_a = reinterpret_cast<float*>(A + o_pa);
     p->part_b = reinterpret_cast<float*>(A + o_pb);
     p->fused = fused_supported(cfg.dim / 32) && fused_supported(cfg.hidden_dim / 32) && cfg.dim / 32 <= 128 &&
                cfg.hidden_dim % 32 == 0 && cfg.dim % 32 == 0 && (p->kvd % 32) == 0;

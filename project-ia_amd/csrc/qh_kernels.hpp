@@ -54,6 +54,9 @@ struct GemvDecode {
     // multiplied by newton(rsqrt(sum/N + eps)) before the epilogue.
     const float* in_part = nullptr;
     float eps = 0.0f;
+    // fp32-input GEMV only: RMSNorm weight of x.  The kernel then converts
+    // x*norm_w and scales every row by newton(rsqrt(sum(x^2)/N + eps)).
+    const float* norm_w = nullptr;
 };
 
 // y = W . x for up to 4 segments sharing the same x (digit planes xd).
@@ -64,7 +67,7 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4
 // are prepared into ws (xd_bytes(N/32) bytes) by a separate launch first.
 constexpr uint32_t kGemvF32MaxBlk = 512;
 hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws,
-                           hipStream_t s);
+                           hipStream_t s, const GemvDecode* dec = nullptr);
 
 // ---- batched prefill GEMM (k_gemm.hip) ----
 // Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 or 2) matrices sharing
