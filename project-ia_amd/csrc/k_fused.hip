@@ -1,20 +1,19 @@
-// k_fused.hip -- the decode step's Q4_0 GEMVs with their neighbours folded
-// into prologue and epilogue, so a Llama-3 layer runs as 7 kernels instead
-// of 10 (no separate RMSNorm/digit or SwiGLU/digit kernels).
+// k_fused.hip -- the decode step's Wo and W_gate|W_up GEMVs with their
+// neighbours folded into prologue and epilogue (no separate RMSNorm/digit
+// or SwiGLU/digit kernels).
 //
 // Every workgroup owns one 32-row block of the output vector (64 matrix rows
 // for W_gate|W_up: the same 32 rows of both), so the epilogue sees a whole
 // 32-element block and can emit the next GEMV's digit planes itself:
-//  * RESID  (Wo, W_down): x_new = res + W.x; stores x_new, the digit planes
-//    of x_new * w_norm (the next RMSNorm's weight) and the block's sum of
+//  * RESID  (Wo): x_new = res + W.x; stores x_new, the digit planes of
+//    x_new * w_norm (the FFN RMSNorm's weight) and the block's sum of
 //    squares of x_new.
-//  * QKV / LOGITS / SWIGLU consume such an input: the RMSNorm scale
-//    r = newton(rsqrt(sum/N + eps)) (reference src/ops/avx2/rmsnorm.c:62-71)
-//    comes from the producer's per-block sums (fixed order), and the
-//    matrix products are scaled by r: W.(r * (x*w)) = r * (W.(x*w)).
-//    QKV then applies RoPE and stores Q and the K/V cache rows; LOGITS stores
-//    the logits; SWIGLU forms h = silu(g)*u (reference silu.c:75-82,
-//    mul_fp32.c) and emits h's digit planes for W_down.
+//  * SWIGLU consumes such an input: the RMSNorm scale r = newton(rsqrt(sum/N
+//    + eps)) (reference src/ops/avx2/rmsnorm.c:62-71) comes from the
+//    producer's per-block sums (fixed order), and the matrix products are
+//    scaled by r: W.(r * (x*w)) = r * (W.(x*w)).  It forms h = silu(g)*u
+//    (reference silu.c:75-82, mul_fp32.c) and emits h's digit planes for
+//    W_down.
 // The dot products are the GEMV's integer digit-plane dots (dot_batch), the
 // K-slices of W waves are summed in LDS in a fixed order, so results are
 // deterministic.  Compared with RMSNorm-then-GEMV the factor r is applied
@@ -33,8 +32,6 @@ namespace qh {
 constexpr int kBufFlagsF = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 typedef uint32_t v4u32f __attribute__((ext_vector_type(4)));
 
-enum : int { kModeQKV = 0, kModeResid = 1, kModeSwiglu = 2, kModeLogits = 3 };
-
 // RMSNorm scale from per-block sums of squares (each lane sums a strided
 // subset in order, then a butterfly; every lane gets the same value).
 __device__ __forceinline__ float norm_scale(const float* __restrict__ part, uint32_t nblk, float eps) {
@@ -49,10 +46,11 @@ __device__ __forceinline__ float norm_scale(const float* __restrict__ part, uint
     return (r0 * (3.0f - a * (r0 * r0))) * 0.5f;
 }
 
-template <int W, int RG, int RT, int J, int MODE>
-__global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
-    constexpr int TR = RG * RT;  // rows per tile: 32, or 64 for SWIGLU
-    static_assert(MODE == kModeSwiglu ? TR == 64 : TR == 32, "tile must cover one 32-element output block");
+// RESID: one 32-row output block per workgroup, RG row groups of RT rows.
+template <int W, int RG, int RT, int J>
+__global__ __launch_bounds__(64 * W * RG) void k_gemv_resid(const FusedArgs a) {
+    constexpr int TR = RG * RT;
+    static_assert(TR == 32, "tile must cover one 32-element output block");
     __shared__ float red[W][TR];
 
     const int lane = threadIdx.x & 63;
@@ -63,21 +61,8 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
     const uint32_t row_bytes = a.nblk * 20u;
 
     // ---- this wave's rows ----
-    uint32_t sg = 0, m0 = 0;
-    if (MODE == kModeSwiglu) {
-        m0 = t * 32u;
-        sg = (rg * RT >= 32) ? 1u : 0u;
-    } else {
-        uint32_t tbase = 0;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            if (sg + 1 < a.nseg && t >= a.tile_end[sg]) {
-                tbase = a.tile_end[sg];
-                ++sg;
-            }
-        m0 = (t - tbase) * 32u;
-    }
-    const uint32_t M = a.M[sg];
+    const uint32_t m0 = t * 32u;
+    const uint32_t M = a.M[0];
     const uint32_t wrow0 = m0 + (uint32_t)((rg * RT) & 31);
 
     // ---- weight loads first (they depend on nothing) ----
@@ -96,7 +81,7 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
         const uint32_t row = wrow0 + (uint32_t)r;
         const int nrec = row < M ? (int)row_bytes : 0;
         const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(a.w[sg] + (size_t)row * row_bytes), 0, nrec, kBufFlagsF);
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.w[0] + (size_t)row * row_bytes), 0, nrec, kBufFlagsF);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const v4u32f v = __builtin_amdgcn_raw_buffer_load_b128(rs, coff[j], 0, 0);
@@ -106,21 +91,10 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
     }
     // ---- epilogue operands of wave 0 (lanes < 32 own the block's rows) ----
     const uint32_t erow = m0 + (uint32_t)(lane & 31);
-    float e_res = 0.0f, e_w = 0.0f, e_c = 0.0f, e_s = 0.0f;
-    uint32_t pos = 0;
+    float e_res = 0.0f, e_w = 0.0f;
     if (wave == 0) {
-        if (MODE == kModeResid) {
-            e_res = a.res[erow < M ? erow : 0u];
-            e_w = a.wnorm[erow < M ? erow : 0u];
-        }
-        if (MODE == kModeQKV) {
-            pos = *a.pos;
-            if ((a.rope_mask >> sg) & 1u) {
-                const uint32_t hd = a.hd[sg];
-                e_c = a.cos_tab[(size_t)pos * hd + erow % hd];
-                e_s = a.sin_tab[(size_t)pos * hd + erow % hd];
-            }
-        }
+        e_res = a.res[erow < M ? erow : 0u];
+        e_w = a.wnorm[erow < M ? erow : 0u];
     }
     // ---- input digits and the norm scale ----
     uint4 xp[J][6];
@@ -132,8 +106,6 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
         for (int j = 0; j < J; ++j) cols[j] = coff[j] / 20u;
         load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
     }
-    float rs_norm = 1.0f;
-    if (MODE != kModeResid) rs_norm = norm_scale(a.in_part, a.nblk, a.eps);
 
     // ---- dots, per-wave row sums, fixed-order sum over the K-slices ----
     float acc[RT];
@@ -165,43 +137,14 @@ __global__ __launch_bounds__(64 * W * RG) void k_gemv_fused(const FusedArgs a) {
         for (int k2 = 1; k2 < W; ++k2) v += red[k2][lane];
     }
     const bool mine = lane < 32 && erow < M;
-
-    if (MODE == kModeLogits) {
-        if (mine) a.y[0][erow] = rs_norm * v;
-    } else if (MODE == kModeQKV) {
-        const float vr = rs_norm * v;
-        const float pv = __shfl_xor(vr, 1);
-        if (mine) {
-            float o = vr;
-            float* dst = a.y[sg] + erow;
-            const uint32_t hd = a.hd[sg];
-            if (hd) {
-                const uint32_t i = erow % hd;
-                if ((a.rope_mask >> sg) & 1u) {
-                    // Pair (x0, x1) = (row&~1, row|1): y0 = x0*c - x1*s,
-                    // y1 = x1*c + x0*s, products rounded separately.
-                    const float t0 = vr * e_c, t1 = pv * e_s;
-                    o = (erow & 1u) ? t0 + t1 : t0 - t1;
-                }
-                dst = a.y[sg] + (size_t)pos * a.pos_stride[sg] + (size_t)(erow / hd) * a.head_stride[sg] + i;
-            }
-            *dst = o;
-        }
-    } else if (MODE == kModeResid) {
-        const float xn = e_res + v;
-        if (mine) a.y[0][erow] = xn;
-        const float u = xn * e_w;
-        float sq = mine ? xn * xn : 0.0f;
+    const float xn = e_res + v;
+    if (mine) a.y[0][erow] = xn;
+    const float u = xn * e_w;
+    float sq = mine ? xn * xn : 0.0f;
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 32);
-        if (lane == 0) a.out_part[m0 / 32u] = sq;
-        prep_lane(mine ? u : 0.0f, m0 / 32u, lane < 32, a.pad_out, reinterpret_cast<uint32_t*>(a.xd_out));
-    } else {  // kModeSwiglu: lanes 0..31 gate rows, 32..63 up rows
-        const float gu = rs_norm * v;
-        const float up = __shfl(gu, (lane & 31) + 32);
-        const float h = silu_approx(gu) * up;
-        prep_lane(mine ? h : 0.0f, m0 / 32u, lane < 32, a.pad_out, reinterpret_cast<uint32_t*>(a.xd_out));
-    }
+    for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 32);
+    if (lane == 0) a.out_part[m0 / 32u] = sq;
+    prep_lane(mine ? u : 0.0f, m0 / 32u, lane < 32, a.pad_out, reinterpret_cast<uint32_t*>(a.xd_out));
 }
 
 // Persistent W_gate|W_up + SwiGLU: 8 waves of 8 rows walk 64-row tiles (32
@@ -310,49 +253,22 @@ __global__ __launch_bounds__(512) void k_swiglu_p(const FusedArgs a, uint32_t nt
     }
 }
 
-template <int W, int RG, int RT, int J, int MODE>
-static hipError_t run_fused(const FusedArgs& a, uint32_t tiles, hipStream_t s) {
+template <int W, int RG, int RT, int J>
+static hipError_t run_resid(const FusedArgs& a, uint32_t tiles, hipStream_t s) {
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_gemv_fused<W, RG, RT, J, MODE>), dim3(tiles), dim3(64 * W * RG), 0, s, a);
+    hipLaunchKernelGGL((k_gemv_resid<W, RG, RT, J>), dim3(tiles), dim3(64 * W * RG), 0, s, a);
     return hipGetLastError();
 }
 
-// Shape dispatch by input width: nblk <= 64 (J=1), <= 128 (J=2) on one
-// wave per K; up to 448 or 512 blocks (W_down of Llama-3 8B) split over 7
-// or 8 waves, each wave all 32 rows of the tile.
-template <int MODE>
-static hipError_t dispatch(const FusedArgs& a, uint32_t tiles, hipStream_t s) {
-    constexpr int RG1 = MODE == kModeSwiglu ? 16 : 8;
-    if (a.nblk <= 64) return run_fused<1, RG1, 4, 1, MODE>(a, tiles, s);
-    if (a.nblk <= 128) return run_fused<1, RG1, 4, 2, MODE>(a, tiles, s);
-    if (MODE == kModeSwiglu) return hipErrorInvalidValue;
-    if (a.nblk <= 448) return run_fused<7, 1, 32, 1, MODE == kModeSwiglu ? kModeResid : MODE>(a, tiles, s);
-    if (a.nblk <= 512) return run_fused<8, 1, 32, 1, MODE == kModeSwiglu ? kModeResid : MODE>(a, tiles, s);
-    return hipErrorInvalidValue;
-}
-
-static uint32_t fill_tiles(FusedArgs& a) {
-    uint32_t tiles = 0;
-    for (uint32_t i = 0; i < 3; ++i) {
-        if (i < a.nseg) tiles += (a.M[i] + 31u) / 32u;
-        a.tile_end[i] = tiles;
-    }
-    return tiles;
-}
-
-bool fused_supported(uint32_t nblk) { return nblk <= 128 || nblk == 448 || (nblk > 128 && nblk <= 512); }
-
-hipError_t launch_fused_qkv(FusedArgs a, hipStream_t s) {
-    if (a.nseg < 1 || a.nseg > 3 || !a.pos) return hipErrorInvalidValue;
-    for (uint32_t i = 0; i < a.nseg; ++i)
-        if (a.M[i] % 32 != 0 || (a.hd[i] && (a.hd[i] % 32 != 0))) return hipErrorInvalidValue;
-    return dispatch<kModeQKV>(a, fill_tiles(a), s);
-}
+bool fused_supported(uint32_t nblk) { return nblk >= 1 && nblk <= 128; }
 
 hipError_t launch_fused_resid(FusedArgs a, hipStream_t s) {
     a.nseg = 1;
     if (a.M[0] % 32 != 0 || !a.res || !a.wnorm || !a.xd_out || !a.out_part) return hipErrorInvalidValue;
-    return dispatch<kModeResid>(a, fill_tiles(a), s);
+    const uint32_t tiles = a.M[0] / 32u;
+    if (a.nblk <= 64) return run_resid<1, 8, 4, 1>(a, tiles, s);
+    if (a.nblk <= 128) return run_resid<1, 8, 4, 2>(a, tiles, s);
+    return hipErrorInvalidValue;
 }
 
 template <int J>
@@ -381,39 +297,6 @@ hipError_t launch_fused_swiglu(FusedArgs a, hipStream_t s) {
     if (a.nblk <= 64) return run_swiglu_p<1>(a, ntiles, s);
     if (a.nblk <= 128) return run_swiglu_p<2>(a, ntiles, s);
     return hipErrorInvalidValue;
-}
-
-hipError_t launch_fused_logits(FusedArgs a, hipStream_t s) {
-    a.nseg = 1;
-    return dispatch<kModeLogits>(a, fill_tiles(a), s);
-}
-
-// x = embd[token] (reference model.c:1027-1068) with the first layer's
-// RMSNorm input prepared as the RESID epilogue does: digits of x * w_norm
-// and per-block sums of squares.  One 32-lane group per block.
-__global__ __launch_bounds__(256) void k_embed_prep(const float* __restrict__ embd, const uint32_t* __restrict__ tok,
-                                                    uint32_t vocab, uint32_t dim, const float* __restrict__ wnorm,
-                                                    float* __restrict__ x, uint32_t pad, uint32_t* __restrict__ xd,
-                                                    float* __restrict__ part) {
-    uint32_t tk = *tok;
-    tk = tk < vocab ? tk : vocab - 1;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    const bool valid = i < dim;
-    const float xv = valid ? embd[(size_t)tk * dim + i] : 0.0f;
-    if (valid) x[i] = xv;
-    float sq = xv * xv;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 32);
-    if (valid && (i & 31u) == 0) part[i / 32u] = sq;
-    prep_lane(valid ? xv * wnorm[i] : 0.0f, i / 32u, valid, pad, xd);
-}
-
-hipError_t launch_embed_prep(const float* embd, const uint32_t* tok, uint32_t vocab, uint32_t dim,
-                             const float* wnorm, float* x, uint4* xd, float* part, hipStream_t s) {
-    if (dim % 32 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_embed_prep, dim3((dim + 255) / 256), dim3(256), 0, s, embd, tok, vocab, dim, wnorm, x,
-                       xd_pad(dim / 32), reinterpret_cast<uint32_t*>(xd), part);
-    return hipGetLastError();
 }
 
 }  // namespace qh

@@ -551,8 +551,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
     p->amax_ws = reinterpret_cast<float*>(A + o_aw);
     p->part_b = reinterpret_cast<float*>(A + o_pb);
-    p->fused = fused_supported(cfg.dim / 32) && fused_supported(cfg.hidden_dim / 32) && cfg.dim / 32 <= 128 &&
-               cfg.hidden_dim % 32 == 0 && cfg.dim % 32 == 0 && (p->kvd % 32) == 0;
+    p->fused = fused_supported(cfg.dim / 32) && (p->kvd % 32) == 0;
     st->plan = p;
     st->dev_arena = p->arena;
     st->dev_arena_size = bytes;
