@@ -259,8 +259,13 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     // the same LDS space.
     constexpr int kMaxBlk = 64 * J * W;
     constexpr int kThreads = 64 * W * G;
+    // One block column per lane and one wave group (J == 1, G == 1): each
+    // wave converts exactly the 64 blocks its own lanes consume, so staging
+    // and conversion stay inside the wave (no workgroup barrier, digits go
+    // straight to registers).
+    constexpr bool kWaveLocal = J == 1 && G == 1;
     constexpr int kPass = XF ? (kMaxBlk + kThreads - 1) / kThreads : 0;
-    constexpr int kLd = XF ? (kMaxBlk * 8 + kThreads - 1) / kThreads : 0;
+    constexpr int kLd = XF ? (kWaveLocal ? 8 : (kMaxBlk * 8 + kThreads - 1) / kThreads) : 0;
     constexpr int kXs = 36;
     constexpr int kLds = !XF ? 1 : (kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
     __shared__ uint4 lds[kLds];
@@ -273,9 +278,9 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             __builtin_amdgcn_make_buffer_rsrc((void*)a.xnorm_w, 0, a.xnorm_w ? (int)(a.nblk * 128u) : 0, kBufFlags);
 #pragma unroll
         for (int i = 0; i < kLd; ++i) {
-            const uint32_t off = ((uint32_t)(i * kThreads) + threadIdx.x) * 16u;
-            xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-            wl[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+            const uint32_t f = kWaveLocal ? (uint32_t)(kw * 512 + i * 64 + lane) : (uint32_t)(i * kThreads) + threadIdx.x;
+            xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, f * 16u, 0, 0);
+            wl[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, f * 16u, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     } else {
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < kLd; ++i) {
-            const uint32_t f = (uint32_t)(i * kThreads) + threadIdx.x;
+            const uint32_t f = kWaveLocal ? (uint32_t)(kw * 512 + i * 64 + lane) : (uint32_t)(i * kThreads) + threadIdx.x;
             v4u32 v = xl[i];
             float x0 = __uint_as_float(v[0]), x1 = __uint_as_float(v[1]);
             float x2 = __uint_as_float(v[2]), x3 = __uint_as_float(v[3]);
@@ -313,7 +318,10 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
             if (lane == 0) lds_ss[wave] = ss;
         }
-        __syncthreads();
+        // Wave-local staging needs no barrier: a wave's LDS writes and the
+        // reads that follow them are ordered (the norm's cross-wave sum is
+        // the only workgroup-wide step, and norm is uniform).
+        if (!kWaveLocal || norm) __syncthreads();
         if (norm) {
             float tot = lds_ss[0];
 #pragma unroll
@@ -321,6 +329,24 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             const float av = tot / (float)(a.nblk * 32u) + a.eps;
             const float r0 = __builtin_amdgcn_rsqf(av);
             rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
+        }
+        if constexpr (kWaveLocal) {
+            float xw[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const v4u32 v = *reinterpret_cast<const v4u32*>(xs + (uint32_t)(kw * 64 + lane) * kXs + (uint32_t)i * 4u);
+                xw[4 * i] = __uint_as_float(v[0]);
+                xw[4 * i + 1] = __uint_as_float(v[1]);
+                xw[4 * i + 2] = __uint_as_float(v[2]);
+                xw[4 * i + 3] = __uint_as_float(v[3]);
+            }
+            uint4 o[7];
+            prep_block(xw, o);
+#pragma unroll
+            for (int p = 0; p < 6; ++p) xp[0][p] = o[p];
+            kk[0] = ok[0] ? (int)o[6].x : 0;
+            zz[0] = ok[0] ? __uint_as_float(o[6].y) : 0.0f;
+            return;
         }
         float xv[kPass > 0 ? kPass : 1][32];
 #pragma unroll

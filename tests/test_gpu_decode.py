@@ -174,3 +174,23 @@ def test_build_graph_rejects_unbuilt_configs(qa, tmp_path):
         qa.synthetic.write_synthetic_model(path, h, 16)
         with pytest.raises(qa.QorusError, match="INVALID_CONFIG"):
             qa.Model(path)
+
+
+def test_decode_unfused_d8448(qa, tmp_path):
+    """d_model 8448 (264 blocks): Q|K|V and the LM head take fp32 x with the
+    RMSNorm in the prologue of the 7-wave GEMV, whose lanes each convert the
+    one block they consume (GQA 66/33)."""
+    h = qa.QorusHeader(vocab=256, dim=8448, hidden=512, n_layers=1, n_heads=66, n_kv=33, max_seq=16)
+    P = 5
+    m, blob, kv = build(qa, tmp_path, h, 17, P, name="d8448.qorus")
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        t = 3
+        for pos in range(P, P + 2):
+            tok_ref, lg_ref = ref.step(t, pos)
+            lg = m.forward([t], pos)
+            assert rel_err(lg, lg_ref) <= 1e-4, pos
+            assert int(np.argmax(lg)) == tok_ref
+            t = tok_ref
+    finally:
+        m.close()
