@@ -223,9 +223,13 @@ __device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, ui
 // wave's time follows its number of tiles: splitting rows into smaller,
 // evenly balanced pieces adds steps and measured slower.
 // ---------------------------------------------------------------------------
-template <int W, int J, int G, int RT, bool XF>
+// SW: SwiGLU pair mode (W == 1): tile u holds rows i0..i0+RT/2-1 of w[0]
+// (W_gate) followed by the same rows of w[1] (W_up), i0 = u*RT/2, and stores
+// h[i] = silu(g_i) * u_i (reference silu.c:75-82, mul_fp32.c) to y[0].
+template <int W, int J, int G, int RT, bool XF, bool SW = false>
 __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     static_assert(W == 1 || G == 1, "multi-wave K split runs one tile per workgroup");
+    static_assert(!SW || (W == 1 && RT % 2 == 0), "SwiGLU pairs need one wave per group and even tiles");
     const int lane = threadIdx.x & 63;
     // The wave index is uniform per wave; readfirstlane makes that visible to
     // the compiler so tile/segment bookkeeping stays scalar (a vector load of
@@ -397,6 +401,24 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         float res, c, sn;
     };
     auto load_tile = [&](uint32_t u, uint4 (&q)[RT][J], float (&s)[RT][J], Epi& e) {
+        if constexpr (SW) {
+            const uint32_t M = a.M[0], i0 = u * (uint32_t)(RT / 2);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const uint32_t row = i0 + (uint32_t)(r % (RT / 2));
+                const int nrec = row < M ? (int)row_bytes : 0;
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)(a.w[r < RT / 2 ? 0 : 1] + (size_t)row * row_bytes), 0, nrec, kBufFlags);
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(rs, coff[j], 0, 0);
+                    q[r][j] = make_uint4(v[0], v[1], v[2], v[3]);
+                    s[r][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, coff[j] + 16u, 0, 0));
+                }
+            }
+            e.res = e.c = e.sn = 0.0f;
+            return;
+        }
         uint32_t sg, tbase;
         seg_of(a, u, sg, tbase);
         const uint8_t* __restrict__ wseg = a.w[sg];
@@ -443,6 +465,19 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
             acc[r] = v * rs_norm;
+        }
+        if constexpr (SW) {
+            const uint32_t i = u * (uint32_t)(RT / 2) + (uint32_t)lane;
+            if (lane < RT / 2 && i < a.M[0]) {
+                float g = acc[0], up = acc[RT / 2];
+#pragma unroll
+                for (int r = 1; r < RT / 2; ++r) {
+                    g = (r == lane) ? acc[r] : g;
+                    up = (r == lane) ? acc[r + RT / 2] : up;
+                }
+                a.y[0][i] = silu_approx(g) * up;
+            }
+            return;
         }
         uint32_t sg, tbase;
         seg_of(a, u, sg, tbase);
@@ -733,12 +768,12 @@ static int num_cu() {
 }
 
 // Persistent grid: as many groups of G tiles as are resident at once.
-template <int W, int J, int G, int RT, bool XF>
+template <int W, int J, int G, int RT, bool XF, bool SW = false>
 static hipError_t launch_gemv_p(const GemvArgs& a, uint32_t tiles, hipStream_t s) {
     static int occ = 0;
     if (occ == 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT, XF>, 64 * W * G, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT, XF, SW>, 64 * W * G, 0) != hipSuccess ||
             o < 1)
             o = 1;
         occ = o;
@@ -746,7 +781,7 @@ static hipError_t launch_gemv_p(const GemvArgs& a, uint32_t tiles, hipStream_t s
     const uint32_t groups = (tiles + G - 1) / G;
     const uint32_t resident = (uint32_t)(occ * num_cu());
     const uint32_t grid = groups < resident ? groups : resident;
-    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT, XF>), dim3(grid), dim3(64 * W * G), 0, s, a);
+    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT, XF, SW>), dim3(grid), dim3(64 * W * G), 0, s, a);
     return hipGetLastError();
 }
 
@@ -801,6 +836,30 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4
     if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
     if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
     return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, xd, s, dec);
+}
+
+// h = silu(W_gate . n) * (W_up . n), n = RMSNorm(x) with weight norm_w (the
+// norm made in the prologue, the factor applied to both products), from the
+// fp32 x[N], N <= 4096 (nblk <= 128).
+hipError_t launch_gemv_swiglu(const uint8_t* w_gate, const uint8_t* w_up, uint32_t M, uint32_t N, const float* x,
+                              const float* norm_w, float eps, float* h, hipStream_t s) {
+    if (N == 0 || N % 32 != 0 || N / 32 > 128 || !w_gate || !w_up || !x || !norm_w || !h) return hipErrorInvalidValue;
+    GemvArgs a{};
+    a.w[0] = w_gate;
+    a.w[1] = w_up;
+    a.y[0] = h;
+    a.M[0] = M;
+    constexpr int kRT = 2;  // one gate and one up row per tile: one element of h
+    const uint32_t tiles = (M + kRT / 2 - 1) / (kRT / 2);
+    a.tile_end[0] = a.tile_end[1] = a.tile_end[2] = a.tile_end[3] = tiles;
+    a.nseg = 1;
+    a.nblk = N / 32;
+    a.pad = xd_pad(a.nblk);
+    a.xf = x;
+    a.xnorm_w = norm_w;
+    a.eps = eps;
+    if (tiles == 0) return hipSuccess;
+    return launch_gemv_p<1, 2, 4, kRT, true, true>(a, tiles, s);
 }
 
 // fp32 input: inputs of up to kGemvF32MaxBlk blocks are converted inside the

@@ -26,7 +26,6 @@
 #include <vector>
 
 #include "qh_decode.hpp"
-#include "qh_fused.hpp"
 #include "qh_kernels.hpp"
 #include "qh_runtime.hpp"
 
@@ -57,8 +56,7 @@ struct ModelPlan {
     uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
     uint32_t hist_cap = 0;
     float* amax_ws = nullptr;                // multi-workgroup argmax partials
-    float* part_b = nullptr;                 // per-block sums of squares of the FFN RMSNorm input
-    bool fused = false;                      // 7-kernel layers (k_fused.hip)
+    bool fused = false;                      // 7-kernel layers (fp32-input GEMVs with fused prologues)
     float* kv = nullptr;
     size_t kv_layer_floats = 0;
     hipStream_t stream = nullptr;
@@ -134,11 +132,12 @@ static q_tensor* make_view(q_context* ctx, size_t offset, uint32_t n0, uint32_t 
 // ---------------------------------------------------------------------------
 // Decode step enqueue (all kernels on p->stream)
 // ---------------------------------------------------------------------------
-// One decode step with the fused kernels: per layer QKV (RMSNorm and digits
-// in the prologue, RoPE and KV stores in the epilogue), attention (3
-// kernels: the reference's clamped polynomial exp needs the global max
-// before any exponential), Wo (+residual, the FFN norm's digits and block sums), gate|up
-// (+norm scale, SwiGLU, digits), down (+residual).
+// One decode step in 7 kernels per layer: Q|K|V from fp32 x (RMSNorm and
+// digits in the prologue, RoPE and KV-cache stores in the epilogue),
+// attention (3 kernels: the reference's clamped polynomial exp needs the
+// global max before any exponential; the combine emits o's digits), Wo +
+// residual, W_gate|W_up from fp32 x1 (FFN RMSNorm in the prologue, SwiGLU
+// in the epilogue, fp32 h out), W_down from fp32 h + residual.
 static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
     const q_llama_config& c = p->cfg;
     hipStream_t s = p->stream;
@@ -148,7 +147,7 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
         e = (x);                         \
         if (e != hipSuccess) return e;   \
     } while (0)
-    const uint32_t nblk_d = c.dim / 32, nblk_h = c.hidden_dim / 32;
+    const uint32_t nblk_d = c.dim / 32;
     QH_E(launch_embed(p->embd, p->tok, c.vocab_size, c.dim, p->x, s));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const LayerDev& L = p->layers[l];
@@ -193,33 +192,14 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
         aa.o_out = nullptr;
         aa.xd_out = p->xd_b;
         QH_E(launch_attention(aa, s));
-        FusedArgs fo;
-        fo.w[0] = L.wo;
-        fo.M[0] = c.dim;
-        fo.nblk = nblk_d;
-        fo.pad = xd_pad(nblk_d);
-        fo.xd = p->xd_b;
-        fo.y[0] = p->x1;
-        fo.res = p->x;
-        fo.wnorm = L.ffn_norm;
-        fo.xd_out = p->xd_a;
-        fo.pad_out = xd_pad(nblk_d);
-        fo.out_part = p->part_b;
-        QH_E(launch_fused_resid(fo, s));
-        FusedArgs fg;
-        fg.w[0] = L.wg;
-        fg.w[1] = L.wu;
-        fg.M[0] = fg.M[1] = c.hidden_dim;
-        fg.nblk = nblk_d;
-        fg.pad = xd_pad(nblk_d);
-        fg.xd = p->xd_a;
-        fg.in_part = p->part_b;
-        fg.eps = c.rms_norm_eps;
-        fg.xd_out = p->xd_c;
-        fg.pad_out = xd_pad(nblk_h);
-        QH_E(launch_fused_swiglu(fg, s));
+        // Wo + residual on the attention output's digits.
+        GemvSeg wo{L.wo, p->x1, p->x, c.dim};
+        QH_E(launch_gemv(&wo, 1, nblk_d, p->xd_b, s));
+        // h = silu(W_gate.n) * (W_up.n), n = RMSNorm(x1) made in the prologue.
+        QH_E(launch_gemv_swiglu(L.wg, L.wu, c.hidden_dim, c.dim, p->x1, L.ffn_norm, c.rms_norm_eps, p->g, s));
+        // W_down + residual straight from the fp32 h.
         GemvSeg wd{L.wd, p->x, p->x1, c.dim};
-        QH_E(launch_gemv(&wd, 1, nblk_h, p->xd_c, s));
+        QH_E(launch_gemv_f32(&wd, 1, c.hidden_dim, p->g, nullptr, s));
     }
     // LM head of RMSNorm(x), the norm made in the GEMV's prologue.
     GemvDecode dn;
@@ -518,7 +498,6 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
     const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
     const size_t o_aw = carve(argmax_workspace_bytes(cfg.vocab_size));
-    const size_t o_pb = carve(cfg.dim / 32 * 4);
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
@@ -550,8 +529,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
     p->amax_ws = reinterpret_cast<float*>(A + o_aw);
-    p->part_b = reinterpret_cast<float*>(A + o_pb);
-    p->fused = fused_supported(cfg.dim / 32) && (p->kvd % 32) == 0;
+    p->fused = cfg.dim / 32 <= 128 && cfg.hidden_dim / 32 <= kGemvF32MaxBlk && (p->kvd % 32) == 0;
     st->plan = p;
     st->dev_arena = p->arena;
     st->dev_arena_size = bytes;

@@ -66,6 +66,10 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4
 // blocks are converted to digit planes inside the GEMV launch; wider ones
 // are prepared into ws (xd_bytes(N/32) bytes) by a separate launch first.
 constexpr uint32_t kGemvF32MaxBlk = 512;
+// h[M] = silu(W_gate . n) * (W_up . n) with n = RMSNorm(x, norm_w, eps) made
+// in the GEMV's prologue (x fp32, N <= 4096): the decode step's FFN input.
+hipError_t launch_gemv_swiglu(const uint8_t* w_gate, const uint8_t* w_up, uint32_t M, uint32_t N, const float* x,
+                              const float* norm_w, float eps, float* h, hipStream_t s);
 hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws,
                            hipStream_t s, const GemvDecode* dec = nullptr);
 
