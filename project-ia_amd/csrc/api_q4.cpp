@@ -194,8 +194,9 @@ q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, u
     if (!workspace) return Q_ERR_INVALID_ARG;
     Device* d;
     QH_TRY_CODE(device(&d));
-    // The MFMA GEMM kernel faulted the GPU on its first run and the cause is
-    // not established; the entry point refuses to launch it until it is.
+    // The kernel has not yet run correctly on a GPU (its first runs were
+    // called through a ctypes binding that truncated Y to 32 bits); the entry
+    // point refuses to launch it until it has.
     if (!kGemmEnabled) return fail(hipErrorNotSupported, "qh_gemm: prefill GEMM kernel disabled");
     QH_TRY(launch_gemm(w, y, M, (int)n, Ws[0]->ne[1], X, T, workspace, (hipStream_t)s));
     return Q_OK;

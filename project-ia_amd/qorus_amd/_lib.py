@@ -182,7 +182,6 @@ def _optional_sigs(L):
         ("q_sample_token", i32, vp, u32, f32, u32, f32, vp, vp),
         ("qh_llama_generate", i32, vp, vp, u32, u32, u32, vp, vp),
         ("qh_attention_decode", i32, vp, vp, vp, u32, u32, u32, u32, u32, vp),
-        ("qh_gemm_q4_f32", i32, vp, vp, vp, u32, vp, vp),
         ("qh_fill_synthetic", i32, vp, u64, u32, u64, vp),
     ]
     for name, res, *args in opt:

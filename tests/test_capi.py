@@ -47,6 +47,74 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, n)
 
 
+def declared_prototypes():
+    """{name: (return kind, [parameter kinds])} from include/*.h, each type
+    reduced to its ABI class: "ptr" (any pointer or handle), "i32", "u32",
+    "u64", "f32", "void"."""
+    scalar = {"int": "i32", "uint32_t": "u32", "uint64_t": "u64", "size_t": "u64", "float": "f32", "void": "void"}
+    types = (REPO / "include" / "qorus_types.h").read_text()
+    for enum in re.findall(r"typedef\s+enum\s*\{[^}]*\}\s*(\w+)\s*;", types):
+        scalar[enum] = "i32"
+    handles = {"qh_stream", "qh_event", "qh_graph"}
+
+    def kind(decl):
+        decl = re.sub(r"\b(const|Q_RESTRICT)\b", " ", decl)
+        if "*" in decl:
+            return "ptr"
+        words = decl.split()
+        base = words[0]
+        if base in handles:
+            return "ptr"
+        return scalar[base]
+
+    protos = {}
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"^([A-Za-z_][\w \*]*?)\b((?:q|qh|llama)_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+            params = [p.strip() for p in m.group(3).split(",") if p.strip()]
+            if params == ["void"]:
+                params = []
+            protos[m.group(2)] = (kind(m.group(1)), [kind(p) for p in params])
+    return protos
+
+
+def ctypes_kind(t):
+    if t is None:
+        return "void"
+    if t in (C.c_void_p, C.c_char_p) or issubclass(t, C._Pointer):
+        return "ptr"
+    if t is C.c_float:
+        return "f32"
+    if t in (C.c_int, C.c_int32):
+        return "i32"
+    if t in (C.c_uint32, C.c_uint):
+        return "u32"
+    if t in (C.c_uint64, C.c_size_t, C.c_ulonglong, C.c_ulong):
+        return "u64"
+    raise AssertionError(f"unmapped ctypes type {t}")
+
+
+def test_ctypes_bindings_match_declarations():
+    """Every ctypes binding in qorus_amd._lib has the argument and return
+    classes of its declaration.  A binding that passes a pointer through a
+    32-bit integer slot truncates the device address, and the kernel then
+    writes to an unmapped one."""
+    protos = declared_prototypes()
+    assert len(protos) >= 40
+    lib = qa.lib()
+    checked = 0
+    for name, (ret, params) in protos.items():
+        fn = getattr(lib, name)
+        if fn.argtypes is None:
+            continue
+        got = [ctypes_kind(t) for t in fn.argtypes]
+        assert got == params, f"{name}: bound {got}, declared {params}"
+        assert ctypes_kind(fn.restype) == ret, f"{name}: returns {fn.restype}, declared {ret}"
+        checked += 1
+    assert checked >= 40
+
+
 def test_strerror_table():
     lib = qa.lib()
     assert lib.q_strerror(0) == b"Success"
