@@ -221,7 +221,10 @@ __device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, ui
 // resident, so there is one wave of workgroups and no per-tile prologue.
 // Each tile step costs about one HBM latency (one tile of prefetch), so a
 // wave's time follows its number of tiles: splitting rows into smaller,
-// evenly balanced pieces adds steps and measured slower.
+// evenly balanced pieces adds steps and measured slower.  The weight loads
+// keep the default cache policy: the non-temporal hint made this kernel 4-10 %
+// slower (a block's 16-byte nibble load and its 4-byte scale load share
+// cache lines), although it speeds up plain one-pass 16-byte reads.
 // ---------------------------------------------------------------------------
 // SW: SwiGLU pair mode (W == 1): tile u holds rows i0..i0+RT/2-1 of w[0]
 // (W_gate) followed by the same rows of w[1] (W_up), i0 = u*RT/2, and stores
