@@ -183,6 +183,18 @@ q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, v
 q_error_code qh_llama_generate(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
                                uint32_t n_steps, uint32_t* tokens_out, float* ms_per_step);
 
+/* ---- Sampling ---- */
+
+/* q_sample_token (qorus.h; reference src/main.c:852-992) runs on the GPU:
+ * temperature softmax, top-k, top-p and the CDF draw with the reference's
+ * arithmetic, validation and arena use.  Its uniform draws come from a
+ * per-thread xorshift64* state that starts at 123456789, as the
+ * reference's.  These two calls set and read the calling thread's state
+ * (no reference counterpart: the reference's state is private; they make a
+ * sampled run reproducible). */
+void qh_sample_set_state(uint64_t state);
+uint64_t qh_sample_get_state(void);
+
 #ifdef __cplusplus
 }
 #endif

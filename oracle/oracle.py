@@ -166,8 +166,72 @@ def lib():
         L.or_gemm_q4_rows.argtypes = [_u8p, C.c_uint32, C.c_uint32, _f32p, C.c_uint32, _f32p]
         L.or_decode_step.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, _f32p]
         L.or_decode_step.restype = C.c_uint32
+        L.or_sample_token.argtypes = [C.c_void_p, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_int, C.c_int,
+                                      C.POINTER(C.c_uint64)]
+        L.or_sample_token.restype = C.c_uint32
         _lib = L
     return _lib
+
+
+class QContext(C.Structure):
+    """q_context (reference include/qorus_types.h:216-231), 72 bytes."""
+    _fields_ = [("weights_mmap", C.c_void_p), ("weights_size", C.c_size_t), ("header", C.c_void_p),
+                ("kv_buffer", C.c_void_p), ("kv_size", C.c_size_t),
+                ("scratch_buffer", C.c_void_p), ("scratch_size", C.c_size_t),
+                ("scratch_head", C.c_size_t), ("scratch_base_offset", C.c_size_t)]
+
+
+RNG_SEED = 123456789  # the reference sampler's initial xorshift64* state (main.c:949)
+
+
+def sample_token(logits: np.ndarray, temperature: float, top_k: int, top_p: float, state: C.c_uint64,
+                 nucleus_all: bool = False) -> int:
+    """or_sample_token on a float32 array (its data address decides the
+    reference's aligned temperature path); state is advanced."""
+    assert logits.dtype == np.float32 and logits.flags.c_contiguous
+    aligned = int(logits.ctypes.data % 32 == 0)
+    return int(lib().or_sample_token(logits.ctypes.data, logits.size, temperature, top_k, top_p, aligned,
+                                     int(nucleus_all), C.byref(state)))
+
+
+class RefSampler:
+    """A private copy of oracle/_ref's library (its own thread-local RNG
+    state, starting at RNG_SEED) with an arena-backed q_context, calling
+    the reference's own q_sample_token."""
+
+    def __init__(self, tmp_dir, arena_bytes: int = 64 << 20):
+        import shutil
+        import uuid
+        # a new file per instance: copying over a library that is still
+        # mapped would corrupt it
+        path = Path(tmp_dir) / f"libqorus_ref_{uuid.uuid4().hex}.so"
+        shutil.copy(_REF, path)
+        R = C.CDLL(str(path))
+        R.q_alloc_arena.argtypes = [C.c_void_p, C.c_size_t]
+        R.q_alloc_arena.restype = C.c_int
+        R.q_arena_reset.argtypes = [C.c_void_p]
+        R.q_arena_reset.restype = None
+        R.q_free_memory.argtypes = [C.c_void_p]
+        R.q_free_memory.restype = None
+        R.q_sample_token.argtypes = [C.c_void_p, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_void_p,
+                                     C.c_void_p]
+        R.q_sample_token.restype = C.c_int
+        self.R = R
+        self.ctx = QContext()
+        if arena_bytes:
+            assert R.q_alloc_arena(C.byref(self.ctx), arena_bytes) == Q_OK
+
+    def sample(self, logits: np.ndarray, temperature: float, top_k: int, top_p: float, reset: bool = True):
+        """(return code, token); the arena is reset first unless reset=False."""
+        if reset and self.ctx.scratch_buffer:
+            self.R.q_arena_reset(C.byref(self.ctx))
+        tok = C.c_uint32(0xFFFFFFFF)
+        ctx = C.byref(self.ctx) if self.ctx.scratch_buffer else None
+        rc = self.R.q_sample_token(logits.ctypes.data, logits.size, temperature, top_k, top_p, C.byref(tok), ctx)
+        return rc, tok.value
+
+    def close(self):
+        self.R.q_free_memory(C.byref(self.ctx))
 
 
 def ref_available() -> bool:

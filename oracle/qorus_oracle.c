@@ -26,6 +26,16 @@
  *   or_silu/softmax    bit-equality with oracle/_ref on the vector part; the
  *                      N%8 tails use libm expf (unpinned libm boundary).
  *   or_argmax          brute force + first-index-on-ties cases.
+ *   or_sample_token    token-for-token equality with oracle/_ref's own
+ *                      q_sample_token (reference src/main.c compiled from its
+ *                      sources, arena path, a fresh RNG state per library
+ *                      copy) on inputs whose top-k/top-p cut has no ties, for
+ *                      temperatures, top-k, top-p and aligned/unaligned
+ *                      logits; the reference's own property tests
+ *                      (tests/test_main.c).  Its two rules for what the
+ *                      reference leaves to its sort internals or to unwritten
+ *                      memory (ties at a cut keep lower indices; no filter
+ *                      keeps every token) have no reference fixture.
  *   or_add/mul         bit-equality with oracle/_ref.
  *   or_dot_f32/matmul  bit-equality with oracle/_ref's q_matmul_f32_avx2.
  *   or_attention_decode  composition of the above; fp64 textbook attention
@@ -284,6 +294,152 @@ void or_softmax(const float* x, float* y, uint32_t N) {
     }
     const float inv = 1.0f / sum;
     for (uint32_t i = 0; i < N; i++) y[i] = y[i] * inv;
+}
+
+/* Sampling.  Reference src/main.c:311-992 (q_sample_token with an arena:
+ * compute_softmax_with_temp, apply_top_k, apply_top_p with
+ * find_nucleus_size_optimized_soa's binary search over the full prefix
+ * sums, the xorshift64* draw, sample_from_distribution), restated with
+ * (p desc, index asc) ordering where the reference's quickselect/quicksort
+ * leave equal probabilities in an order of their own, and every token valid
+ * when neither filter is on (the reference reads an unwritten mask). */
+typedef struct {
+    uint32_t key, idx;
+} or_kv;
+
+static int or_kv_desc(const void* a, const void* b) {
+    const or_kv* x = (const or_kv*)a;
+    const or_kv* y = (const or_kv*)b;
+    if (x->key != y->key) return x->key > y->key ? -1 : 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx ? 1 : 0);
+}
+
+static void or_sort_desc(const float* p, uint32_t V, or_kv* kv) {
+    for (uint32_t i = 0; i < V; i++) {
+        uint32_t b;
+        memcpy(&b, &p[i], 4);
+        kv[i].key = b == 0x80000000u ? 0u : b;
+        kv[i].idx = i;
+    }
+    qsort(kv, V, sizeof(or_kv), or_kv_desc);
+}
+
+uint32_t or_sample_token(const float* logits, uint32_t V, float temperature, uint32_t top_k, float top_p,
+                         int logits_aligned, int nucleus_all, uint64_t* state) {
+    float* sc = (float*)malloc((size_t)V * sizeof(float));
+    float* p = (float*)malloc((size_t)V * sizeof(float));
+    float* cs = (float*)malloc((size_t)V * sizeof(float));
+    uint8_t* m = (uint8_t*)malloc(V);
+    or_kv* kv = (or_kv*)malloc((size_t)V * sizeof(or_kv));
+    /* temperature: 8-wide part times 1/T when the logits are aligned,
+     * the rest divided (main.c:338-365) */
+    const float inv = 1.0f / temperature;
+    const uint32_t n_mul = (V >= 8 && logits_aligned) ? (V & ~7u) : 0u;
+    for (uint32_t i = 0; i < V; i++) sc[i] = i < n_mul ? logits[i] * inv : logits[i] / temperature;
+    /* softmax: q_softmax_f32_avx2 for V >= 8 (main.c:371-385), else the
+     * sampler's scalar fallback (main.c:389-424) */
+    if (V >= 8) {
+        or_softmax(sc, p, V);
+    } else {
+        float mx = sc[0];
+        for (uint32_t i = 1; i < V; i++)
+            if (sc[i] > mx) mx = sc[i];
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < V; i++) {
+            p[i] = expf(sc[i] - mx);
+            sum += p[i];
+        }
+        if (sum > 0.0f) {
+            const float is = 1.0f / sum;
+            for (uint32_t i = 0; i < V; i++) p[i] *= is;
+        } else {
+            const float u = 1.0f / (float)V;
+            for (uint32_t i = 0; i < V; i++) p[i] = u;
+        }
+    }
+    int mask_set = 0;
+    /* top-k (main.c:431-521) */
+    if (top_k > 0) {
+        if (top_k >= V) {
+            memset(m, 1, V);
+        } else {
+            or_sort_desc(p, V, kv);
+            memset(m, 0, V);
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < top_k; j++) {
+                m[kv[j].idx] = 1;
+                sum += p[kv[j].idx];
+            }
+            if (sum > 0.0f)
+                for (uint32_t i = 0; i < V; i++) p[i] = m[i] ? p[i] / sum : 0.0f;
+        }
+        mask_set = 1;
+    }
+    /* top-p (main.c:720-808, 525-597) */
+    if (top_p > 0.0f) {
+        if (top_p >= 1.0f) {
+            memset(m, 1, V);
+        } else {
+            or_sort_desc(p, V, kv);
+            uint32_t best = V;
+            if (!nucleus_all) {
+                cs[0] = p[kv[0].idx];
+                for (uint32_t j = 1; j < V; j++) cs[j] = cs[j - 1] + p[kv[j].idx];
+                uint32_t left = 1, right = V;
+                while (left <= right) {
+                    const uint32_t mid = left + (right - left) / 2;
+                    if (cs[mid - 1] >= top_p) {
+                        best = mid;
+                        right = mid - 1;
+                    } else {
+                        left = mid + 1;
+                    }
+                }
+            }
+            memset(m, 0, V);
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < best; j++) {
+                m[kv[j].idx] = 1;
+                sum += p[kv[j].idx];
+            }
+            if (sum > 0.0f)
+                for (uint32_t i = 0; i < V; i++) p[i] = m[i] ? p[i] / sum : 0.0f;
+        }
+        mask_set = 1;
+    }
+    if (!mask_set) memset(m, 1, V);
+    /* xorshift64* draw (main.c:949-968) */
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    const uint32_t u32 = (uint32_t)((x * 0x2545F4914F6CDD1DULL) >> 32);
+    const float r = (float)(u32 >> 8) / 16777216.0f;
+    /* CDF walk over valid tokens in index order (main.c:811-849) */
+    uint32_t tok = V - 1;
+    int found = 0;
+    float c = 0.0f;
+    for (uint32_t i = 0; i < V && !found; i++)
+        if (m[i]) {
+            c += p[i];
+            if (r < c) {
+                tok = i;
+                found = 1;
+            }
+        }
+    if (!found)
+        for (uint32_t i = V; i > 0; i--)
+            if (m[i - 1]) {
+                tok = i - 1;
+                break;
+            }
+    free(sc);
+    free(p);
+    free(cs);
+    free(m);
+    free(kv);
+    return tok;
 }
 
 /* Greedy argmax.  Reference src/main.c:870-881: first index, strict >. */

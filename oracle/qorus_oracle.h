@@ -47,6 +47,12 @@ float or_exp_approx(float x);
 void or_silu(const float* x, float* y, uint32_t N);
 void or_softmax(const float* x, float* y, uint32_t N);
 uint32_t or_argmax(const float* x, uint32_t N);
+/* q_sample_token, temperature > 0 (reference main.c:311-992, arena path):
+ * *state is the xorshift64* state, advanced once.  logits_aligned: the
+ * caller's logits are 32-byte aligned; nucleus_all: top-p keeps every token
+ * (the reference's prefix-sum allocation failed). */
+uint32_t or_sample_token(const float* logits, uint32_t V, float temperature, uint32_t top_k, float top_p,
+                         int logits_aligned, int nucleus_all, uint64_t* state);
 void or_add(const float* a, const float* b, float* out, uint32_t N);
 void or_mul(const float* a, const float* b, float* out, uint32_t N);
 /* Dot product in the order of q_matmul_f32_avx2's inner loop. */

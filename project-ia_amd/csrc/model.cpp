@@ -594,31 +594,6 @@ q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restr
     return Q_OK;
 }
 
-// Reference src/main.c:852-881, greedy branch, argmax on the GPU.
-q_error_code q_sample_token(const float* __restrict__ logits, uint32_t vocab_size, float temperature,
-                            uint32_t top_k, float top_p, uint32_t* __restrict__ token_id_out,
-                            q_context* __restrict__ ctx) {
-    (void)top_k;
-    (void)top_p;
-    (void)ctx;
-    if (!logits || !token_id_out) return Q_ERR_INVALID_ARG;
-    if (vocab_size == 0) return Q_ERR_INVALID_SIZE;
-    if (!(temperature >= 0.0f) || !std::isfinite(temperature)) return Q_ERR_INVALID_ARG;
-    if (!(temperature < 1e-6f)) return Q_ERR_INVALID_ARG;  // sampling is not part of this build
-    Device* d;
-    QH_TRY_CODE(device(&d));
-    std::lock_guard<std::mutex> lk(d->mu);
-    void* buf;
-    QH_TRY_CODE(stage(d, 1, (size_t)vocab_size * 4 + 256, &buf));
-    float* dl = static_cast<float*>(buf);
-    uint32_t* di = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(buf) + (((size_t)vocab_size * 4 + 255) & ~(size_t)255));
-    QH_TRY(hipMemcpyAsync(dl, logits, (size_t)vocab_size * 4, hipMemcpyHostToDevice, d->stream));
-    QH_TRY(launch_argmax(dl, vocab_size, di, d->stream));
-    QH_TRY(hipMemcpyAsync(token_id_out, di, 4, hipMemcpyDeviceToHost, d->stream));
-    QH_TRY(hipStreamSynchronize(d->stream));
-    return Q_OK;
-}
-
 // Greedy generation on the device: n_steps decode steps from (token, pos),
 // each step's argmax fed back as the next token and the position advanced
 // on the device (no host round trip between steps).  tokens_out (host,

@@ -181,8 +181,8 @@ def _optional_sigs(L):
         ("llama_forward", i32, vp, vp, vp, u32, u32, vp),
         ("q_sample_token", i32, vp, u32, f32, u32, f32, vp, vp),
         ("qh_llama_generate", i32, vp, vp, u32, u32, u32, vp, vp),
-        ("qh_attention_decode", i32, vp, vp, vp, u32, u32, u32, u32, u32, vp),
-        ("qh_fill_synthetic", i32, vp, u64, u32, u64, vp),
+        ("qh_sample_set_state", None, u64),
+        ("qh_sample_get_state", u64),
     ]
     for name, res, *args in opt:
         if hasattr(L, name):
