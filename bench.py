@@ -534,6 +534,39 @@ def traffic_from_profiles():
         return None
 
 
+def run_sample(n_calls=40, warmup=5):
+    """q_sample_token (reference main.c:852-992) at the Llama-3 vocabulary
+    (128256) on synthetic logits, host logits in and token out as the
+    reference's API takes them: wall time per call (H2D of the logits, the
+    device pipeline, the token's D2H), median over n_calls."""
+    import qorus_amd as qa
+    lib = qa.lib()
+    V = 128256
+    rng = np.random.default_rng(12)
+    raw = np.empty(V * 4 + 64, np.uint8)  # 64-byte aligned float32 logits
+    off = (-raw.ctypes.data) % 64
+    lg = raw[off:off + V * 4].view(np.float32)
+    lg[:] = rng.standard_normal(V).astype(np.float32) * np.float32(3.0)
+    tok = C.c_uint32()
+    lib.qh_sample_set_state(123456789)
+    out = {}
+    for name, T, k, p in (("greedy", 0.0, 0, 0.0), ("T0.8_topk40", 0.8, 40, 0.0), ("T0.8_topp0.9", 0.8, 0, 0.9),
+                          ("T0.8_topk40_topp0.95", 0.8, 40, 0.95), ("T1.0_no_filter", 1.0, 0, 0.0)):
+        ts = []
+        for i in range(warmup + n_calls):
+            t0 = time.perf_counter()
+            rc = lib.q_sample_token(lg.ctypes.data, V, T, k, p, C.byref(tok), None)
+            t1 = time.perf_counter()
+            if rc != 0:
+                raise SystemExit(f"q_sample_token failed: {lib.qh_last_error().decode()}")
+            if i >= warmup:
+                ts.append(t1 - t0)
+        out[name] = round(float(np.median(ts)) * 1e6, 1)
+    log(f"[bench] q_sample_token us/call at V={V}: {out}")
+    return {"vocab": V, "us_per_call": out,
+            "logits": "synthetic N(0,1)*3, host memory (the reference API's contract)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +579,7 @@ def main():
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
     ap.add_argument("--no-lmhead", action="store_true", help="skip the config-3 LM-head leg")
+    ap.add_argument("--no-sample", action="store_true", help="skip the q_sample_token leg")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -569,6 +603,7 @@ def main():
     cpu = None if args.no_cpu else run_cpu_baseline(args.cpu_seconds)
     lmhead = None if args.no_lmhead else run_lmhead(args)
     decode = None if args.no_decode else run_decode(args)
+    sample = None if args.no_sample else run_sample()
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -595,6 +630,7 @@ def main():
         "cpu_baseline": cpu,
         "lmhead": lmhead,
         "decode": decode,
+        "sample": sample,
     }
     print(json.dumps(out), flush=True)
 
