@@ -277,6 +277,12 @@ def run_decode(args):
         m.generate(first_tok, DEC_POS, args.decode_warmup)
         m.upload_kv(kv)
         toks, ms = m.generate(first_tok, DEC_POS, steps)
+        # the same decode with each token sampled on the device
+        # (temperature 0.8, top-k 40, top-p 0.95)
+        m.upload_kv(kv)
+        m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
+        m.upload_kv(kv)
+        _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
         m.close()
         avg_ctx = DEC_POS + 1 + (steps - 1) / 2
         bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
@@ -288,7 +294,10 @@ def run_decode(args):
                "hbm_bytes_per_token": bpt,
                "achieved_GB_s": round(bpt / (ms * 1e-3) / 1e9, 1),
                "frac_of_hbm_peak": round(bpt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-               "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1)}
+               "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
+               "sampled_tok_s": round(1e3 / ms_s, 1),
+               "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
+                                   "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
         if not args.no_cpu:
             out["cpu_baseline"], out["first_token_matches_cpu"] = run_cpu_decode(path, kv, first_tok, int(toks[0]),
                                                                                 args.cpu_decode_tokens)

@@ -183,6 +183,18 @@ q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, v
 q_error_code qh_llama_generate(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
                                uint32_t n_steps, uint32_t* tokens_out, float* ms_per_step);
 
+/* Sampled generation on the device (no reference counterpart; the device
+ * form of the q_generate loop, reference src/main.c:994-1131): as
+ * qh_llama_generate, but each step's token is drawn by q_sample_token's
+ * device pipeline (temperature, top_k, top_p with its semantics and
+ * validation) from the logits in HBM, one draw of the calling thread's
+ * sampling RNG per step.  The tokens equal a host loop of llama_forward and
+ * q_sample_token on the same thread with 32-byte-aligned logits.
+ * temperature < 1e-6 is qh_llama_generate. */
+q_error_code qh_llama_generate_sampled(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
+                                       uint32_t n_steps, float temperature, uint32_t top_k, float top_p,
+                                       uint32_t* tokens_out, float* ms_per_step);
+
 /* ---- Sampling ---- */
 
 /* q_sample_token (qorus.h; reference src/main.c:852-992) runs on the GPU:

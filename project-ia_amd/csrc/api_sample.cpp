@@ -50,6 +50,9 @@ bool arena_prob_array(q_context* ctx, uint32_t V) {
 }
 
 }  // namespace
+
+float sample_draw() { return next_uniform(); }
+
 }  // namespace qh
 
 using namespace qh;

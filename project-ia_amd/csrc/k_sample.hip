@@ -359,6 +359,17 @@ __global__ __launch_bounds__(64) void k_pick(const float* __restrict__ p, const 
     if (lane == 0) *token = tok;
 }
 
+// Generation feedback after a sampled token: append it to the history and
+// advance the position (the sampled token itself is already in *tok).
+__global__ void k_feedback(const uint32_t* __restrict__ tok, uint32_t* __restrict__ pos, uint32_t* __restrict__ hist,
+                           uint32_t* __restrict__ hist_n, uint32_t hist_cap) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const uint32_t n = *hist_n;
+    if (n < hist_cap) hist[n] = *tok;
+    *hist_n = n + 1u;
+    *pos += 1u;
+}
+
 inline size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct Layout {
@@ -395,6 +406,12 @@ hipError_t layout_of(uint32_t V, Layout* L) {
 }
 
 }  // namespace
+
+hipError_t launch_token_feedback(const uint32_t* tok, uint32_t* pos, uint32_t* hist, uint32_t* hist_n,
+                                 uint32_t hist_cap, hipStream_t s) {
+    hipLaunchKernelGGL(k_feedback, dim3(1), dim3(64), 0, s, tok, pos, hist, hist_n, hist_cap);
+    return hipGetLastError();
+}
 
 size_t sample_workspace_bytes(uint32_t V) {
     Layout L{};

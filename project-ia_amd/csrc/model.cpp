@@ -28,6 +28,7 @@
 #include "qh_decode.hpp"
 #include "qh_kernels.hpp"
 #include "qh_runtime.hpp"
+#include "qh_sample.hpp"
 
 namespace qh {
 
@@ -62,6 +63,7 @@ struct ModelPlan {
     hipStream_t stream = nullptr;
     hipGraphExec_t step_graph = nullptr;     // decode step, host-fed token/pos
     hipGraphExec_t gen_graph = nullptr;      // decode step + greedy feedback + pos advance
+    void* sample_ws = nullptr;               // device workspace of sampled generation
     uint32_t* pinned = nullptr;              // host staging for token/pos
 };
 
@@ -75,6 +77,7 @@ void plan_destroy(CtxState* st) {
     if (p->step_graph) (void)hipGraphExecDestroy(p->step_graph);
     if (p->gen_graph) (void)hipGraphExecDestroy(p->gen_graph);
     if (p->arena) (void)hipFree(p->arena);
+    if (p->sample_ws) (void)hipFree(p->sample_ws);
     if (p->pinned) (void)hipHostFree(p->pinned);
     if (p->stream) (void)hipStreamDestroy(p->stream);
     delete p;
@@ -623,6 +626,71 @@ q_error_code qh_llama_generate(q_llama_model* model, q_context* ctx, uint32_t to
     QH_TRY(hipEventCreate(&e1));
     QH_TRY(hipEventRecord(e0, p->stream));
     for (uint32_t i = 0; i < n_steps; ++i) QH_TRY(hipGraphLaunch(p->gen_graph, p->stream));
+    QH_TRY(hipEventRecord(e1, p->stream));
+    QH_TRY(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    QH_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (ms_per_step) *ms_per_step = ms / (float)n_steps;
+    QH_TRY(hipMemcpy(tokens_out, p->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
+    return Q_OK;
+}
+
+// Sampled generation on the device (the q_generate loop of reference
+// src/main.c:994-1131 with temperature/top-k/top-p, tokenizer aside): each
+// step is the captured decode step, then q_sample_token's device pipeline
+// on the logits in HBM writing the next token straight into the step's
+// token slot, then the history append and position advance.  The uniform
+// draws come from the calling thread's stream (one per step, in order), so
+// the tokens equal those of a host loop of llama_forward + q_sample_token
+// on the same thread (with 32-byte-aligned host logits, as the reference's
+// arena gives).  temperature < 1e-6 is the greedy qh_llama_generate.
+q_error_code qh_llama_generate_sampled(q_llama_model* model, q_context* ctx, uint32_t token, uint32_t pos,
+                                       uint32_t n_steps, float temperature, uint32_t top_k, float top_p,
+                                       uint32_t* tokens_out, float* ms_per_step) {
+    if (!(temperature >= 0.0f) || !std::isfinite(temperature)) return Q_ERR_INVALID_ARG;
+    if (temperature < 1e-6f) return qh_llama_generate(model, ctx, token, pos, n_steps, tokens_out, ms_per_step);
+    if (!model || !ctx || !tokens_out) return Q_ERR_INVALID_ARG;
+    if (n_steps == 0) return Q_ERR_INVALID_SIZE;
+    if (token >= model->config.vocab_size) return Q_ERR_INVALID_ARG;
+    if ((uint64_t)pos + n_steps > model->config.max_seq_len) return Q_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    ModelPlan* p = plan_of(model, ctx);
+    if (!p) return Q_ERR_INVALID_ARG;
+    QH_TRY_CODE(check_kv(p, ctx));
+    QH_TRY_CODE(bind_kv(p, ctx));
+    if (!p->step_graph) QH_TRY_CODE(capture(p, false, &p->step_graph));
+    const uint32_t V = p->cfg.vocab_size;
+    if (!p->sample_ws) {
+        const size_t wb = sample_workspace_bytes(V);
+        if (wb == 0) return fail(hipErrorInvalidValue, "qh_llama_generate_sampled: workspace size");
+        QH_TRY(hipMalloc(&p->sample_ws, wb));
+    }
+    SampleParams sp;
+    sp.vocab = V;
+    sp.temperature = temperature;
+    sp.inv_temperature = 1.0f / temperature;
+    sp.n_mul = V >= 8 ? (V & ~7u) : 0u;  // device logits are 256-byte aligned
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    QH_TRY(hipStreamSynchronize(p->stream));
+    p->pinned[0] = token;
+    p->pinned[1] = pos;
+    p->pinned[2] = 0;
+    QH_TRY(hipMemcpyAsync(p->tok, &p->pinned[0], 4, hipMemcpyHostToDevice, p->stream));
+    QH_TRY(hipMemcpyAsync(p->pos, &p->pinned[1], 4, hipMemcpyHostToDevice, p->stream));
+    QH_TRY(hipMemcpyAsync(p->hist_n, &p->pinned[2], 4, hipMemcpyHostToDevice, p->stream));
+    hipEvent_t e0, e1;
+    QH_TRY(hipEventCreate(&e0));
+    QH_TRY(hipEventCreate(&e1));
+    QH_TRY(hipEventRecord(e0, p->stream));
+    for (uint32_t i = 0; i < n_steps; ++i) {
+        QH_TRY(hipGraphLaunch(p->step_graph, p->stream));
+        sp.r = sample_draw();
+        QH_TRY(launch_sample(p->logits, sp, p->sample_ws, p->tok, p->stream));
+        QH_TRY(launch_token_feedback(p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->stream));
+    }
     QH_TRY(hipEventRecord(e1, p->stream));
     QH_TRY(hipEventSynchronize(e1));
     float ms = 0.0f;

@@ -19,6 +19,15 @@ struct SampleParams {
     float r = 0.0f;                // uniform draw in [0, 1)
 };
 
+// The calling thread's next uniform draw in [0, 1) (the reference's
+// xorshift64* stream, advanced once).
+float sample_draw();
+
+// After a sampled generation step: hist[*hist_n] = *tok (if it fits),
+// ++*hist_n, ++*pos.
+hipError_t launch_token_feedback(const uint32_t* tok, uint32_t* pos, uint32_t* hist, uint32_t* hist_n,
+                                 uint32_t hist_cap, hipStream_t s);
+
 // Device workspace bytes launch_sample needs for a vocabulary of V.
 size_t sample_workspace_bytes(uint32_t V);
 // Samples one token from device logits[V] into *token (device memory).

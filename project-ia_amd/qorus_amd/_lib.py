@@ -181,6 +181,7 @@ def _optional_sigs(L):
         ("llama_forward", i32, vp, vp, vp, u32, u32, vp),
         ("q_sample_token", i32, vp, u32, f32, u32, f32, vp, vp),
         ("qh_llama_generate", i32, vp, vp, u32, u32, u32, vp, vp),
+        ("qh_llama_generate_sampled", i32, vp, vp, u32, u32, u32, f32, u32, f32, vp, vp),
         ("qh_sample_set_state", None, u64),
         ("qh_sample_get_state", u64),
     ]

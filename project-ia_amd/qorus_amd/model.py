@@ -82,6 +82,17 @@ class Model:
                                       C.byref(ms)), "qh_llama_generate")
         return out, float(ms.value)
 
+    def generate_sampled(self, token: int, pos: int, n: int, temperature: float, top_k: int = 0,
+                         top_p: float = 0.0):
+        """qh_llama_generate_sampled: n device steps, each token sampled on
+        the device (q_sample_token semantics, this thread's RNG stream)."""
+        out = np.empty(n, dtype=np.uint32)
+        ms = C.c_float()
+        check(lib().qh_llama_generate_sampled(C.byref(self.model), C.byref(self.ctx), token, pos, n, temperature,
+                                              top_k, top_p, out.ctypes.data, C.byref(ms)),
+              "qh_llama_generate_sampled")
+        return out, float(ms.value)
+
     def close(self):
         if not self._closed:
             lib().llama_free_graph(C.byref(self.model))

@@ -9,6 +9,8 @@ Bars, written out:
 The GPU and the oracle differ only in floating-point order (GEMV integer
 dots, tree reductions in RMSNorm/softmax/attention sums), see the op tests.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -192,5 +194,36 @@ def test_decode_unfused_d8448(qa, tmp_path):
             assert rel_err(lg, lg_ref) <= 1e-4, pos
             assert int(np.argmax(lg)) == tok_ref
             t = tok_ref
+    finally:
+        m.close()
+
+
+def test_generate_sampled_matches_host_loop(qa, tmp_path):
+    """qh_llama_generate_sampled (sampling on the device, only the tokens
+    leave it) equals a host loop of llama_forward + q_sample_token on the
+    same thread's RNG stream with 32-byte-aligned logits, for temperature
+    with top-k, top-p, both, and neither; temperature 0 is the greedy
+    generation."""
+    h = qa.QorusHeader(vocab=1000, dim=512, hidden=1024, n_layers=2, n_heads=4, n_kv=1, max_seq=256)
+    P, n = 50, 8
+    m, blob, kv = build(qa, tmp_path, h, 21, P)
+    lib = qa.lib()
+    buf = orc.aligned_empty((h.vocab,), np.float32, 64)
+    try:
+        for T, k, p in ((0.8, 40, 0.0), (1.0, 0, 0.9), (0.7, 50, 0.95), (1.2, 0, 0.0), (0.0, 0, 0.0)):
+            m.upload_kv(kv)
+            lib.qh_sample_set_state(2468)
+            toks, ms = m.generate_sampled(7, P, n, T, k, p)
+            assert ms > 0
+            m.upload_kv(kv)
+            lib.qh_sample_set_state(2468)
+            want, t = [], 7
+            for i in range(n):
+                buf[:] = m.forward([t], P + i)
+                out = C.c_uint32()
+                assert lib.q_sample_token(buf.ctypes.data, h.vocab, T, k, p, C.byref(out), None) == 0
+                t = out.value
+                want.append(t)
+            assert toks.tolist() == want, (T, k, p)
     finally:
         m.close()
