@@ -366,18 +366,18 @@ def run_lmhead(args):
     def gemv(t):
         qa.check(lib.qh_gemv_q4_f32_multi(ptr_array([t.addr]), None, ys, 1, x.ptr, ws.ptr, s))
 
-    def softmax():
-        qa.check(lib.qh_softmax_f32(logits.ptr, probs.ptr, VOCAB, s))
+    smx_ws = qa.DeviceBuffer(lib.qh_softmax_workspace_bytes(VOCAB))
 
-    def argmax():
-        qa.check(lib.qh_argmax_f32(logits.ptr, VOCAB, tok.ptr, s))
+    def softmax_argmax():
+        """softmax of the logits and their greedy argmax in the softmax's
+        three passes (results: q_softmax_f32_avx2 and main.c:870-881)."""
+        qa.check(lib.qh_softmax_argmax_f32_ws(logits.ptr, probs.ptr, VOCAB, tok.ptr, smx_ws.ptr, s))
 
     graphs = []
     for t in ts:
         qa.check(lib.qh_stream_begin_capture(s))
         gemv(t)
-        softmax()
-        argmax()
+        softmax_argmax()
         g = C.c_void_p()
         qa.check(lib.qh_stream_end_capture(s, C.byref(g)))
         graphs.append(g.value)
@@ -395,9 +395,9 @@ def run_lmhead(args):
     tk = int(tok.download(np.uint32, (1,))[0])
     ok = tk == int(np.argmax(lg))
     # stage timings with events (eager launches on the same stream)
-    stages = {"gemv": [], "softmax": [], "argmax": []}
+    stages = {"gemv": [], "softmax_argmax": []}
     for i in range(16):
-        for name, fn in (("gemv", lambda: gemv(ts[i % LM_COPIES])), ("softmax", softmax), ("argmax", argmax)):
+        for name, fn in (("gemv", lambda: gemv(ts[i % LM_COPIES])), ("softmax_argmax", softmax_argmax)):
             a, b = qa.Event(), qa.Event()
             a.record(stream)
             fn()

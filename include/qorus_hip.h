@@ -168,6 +168,14 @@ q_error_code qh_mul_f32(const float* a, const float* b, float* output, uint32_t 
 q_error_code qh_argmax_f32(const float* x, uint32_t N, uint32_t* index_out, qh_stream s);
 size_t qh_argmax_workspace_bytes(uint32_t N);
 q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, void* workspace, qh_stream s);
+/* Softmax of x into output and the greedy argmax of x into *index_out in
+ * one pass structure (no reference counterpart: the reference's LM-head
+ * step runs q_softmax_f32_avx2 and the argmax of src/main.c:870-881 one
+ * after the other; results are those two calls').  workspace holds
+ * qh_softmax_workspace_bytes(N) device bytes; x must not alias output
+ * (Q_ERR_ALIASING). */
+q_error_code qh_softmax_argmax_f32_ws(const float* x, float* output, uint32_t N, uint32_t* index_out,
+                                      void* workspace, qh_stream s);
 
 /* ---- Decode on the device ---- */
 

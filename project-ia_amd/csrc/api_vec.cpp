@@ -297,6 +297,17 @@ q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* 
     return Q_OK;
 }
 
+q_error_code qh_softmax_argmax_f32_ws(const float* x, float* output, uint32_t N, uint32_t* index_out,
+                                      void* workspace, qh_stream s) {
+    QH_TRY_CODE(validate_softmax(x, output, N));
+    if (!index_out || !workspace) return Q_ERR_INVALID_ARG;
+    if (x == output) return Q_ERR_ALIASING;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    QH_TRY(launch_softmax_argmax_ws(x, output, N, static_cast<float*>(workspace), index_out, (hipStream_t)s));
+    return Q_OK;
+}
+
 q_error_code qh_add_f32(const float* a, const float* b, float* output, uint32_t N, qh_stream s) {
     if (!a || !b || !output) return Q_ERR_INVALID_ARG;
     Device* d;

@@ -150,14 +150,31 @@ hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s) {
 //      expf(x_i - m) written to y and kept in the workspace;
 //   C: total = per-slice sums in slice order, then the tail values in index
 //      order; inv = 1/total; y_i *= inv.
-// Workspace floats: [0, G) slice max, [G, 2G) slice sums, [2G, 2G+8) tail.
-__global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uint32_t slice, float* ws) {
+// Workspace floats: [0, G) slice max, [G, 2G) slice sums, [2G, 2G+8) tail,
+// [2G+8, 3G+8) the slices' first max indices (fused argmax).
+// With first_idx: also the first index of the slice holding its maximum
+// (0xFFFFFFFF when no element equals it, e.g. an all-NaN slice).
+__global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uint32_t slice, float* ws,
+                                                 uint32_t* first_idx) {
     __shared__ float red[4];
+    __shared__ uint32_t redi[4];
     const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
     float m = -INFINITY;
     for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) m = fmaxf(m, x[i]);
     m = block_max<256>(m, red);
     if (threadIdx.x == 0) ws[blockIdx.x] = m;
+    if (!first_idx) return;
+    uint32_t f = 0xFFFFFFFFu;
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256)
+        if (x[i] == m) {
+            f = i;
+            break;
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) f = min(f, (uint32_t)__shfl_xor((int)f, off));
+    if ((threadIdx.x & 63) == 0) redi[threadIdx.x >> 6] = f;
+    __syncthreads();
+    if (threadIdx.x == 0) first_idx[blockIdx.x] = min(min(redi[0], redi[1]), min(redi[2], redi[3]));
 }
 
 __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint32_t N, uint32_t slice, uint32_t G,
@@ -185,9 +202,26 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
     if (threadIdx.x == 0) ws[G + blockIdx.x] = sum;
 }
 
+// With index_out: block 0 also writes the greedy argmax of x (reference
+// src/main.c:870-881: first index of the maximum, strict >, index 0 when
+// x[0] is NaN or nothing compares greater) from the slice maxima and their
+// first indices.
 __global__ __launch_bounds__(256) void k_smx_norm(float* y, uint32_t N, uint32_t slice, uint32_t G,
-                                                  const float* ws) {
+                                                  const float* ws, const float* x, const uint32_t* first_idx,
+                                                  uint32_t* index_out) {
     __shared__ float inv_s;
+    if (index_out && blockIdx.x == 0 && threadIdx.x == 0) {
+        float m = -INFINITY;
+        for (uint32_t g = 0; g < G; ++g) m = fmaxf(m, ws[g]);
+        uint32_t best = 0;
+        for (uint32_t g = 0; g < G; ++g)
+            if (ws[g] == m && first_idx[g] != 0xFFFFFFFFu) {
+                best = first_idx[g];
+                break;
+            }
+        if (x[0] != x[0]) best = 0;
+        *index_out = best;
+    }
     if (threadIdx.x == 0) {
         float total = 0.0f;
         for (uint32_t g = 0; g < G; ++g) total = total + ws[G + g];
@@ -218,9 +252,29 @@ hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hi
     if (N < kSmxMultiMin || !ws) return launch_softmax(x, y, N, s);
     uint32_t sl, G;
     smx_shape(N, &sl, &G);
-    hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws);
+    hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, (uint32_t*)nullptr);
     hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws);
-    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws, x, (const uint32_t*)nullptr,
+                       (uint32_t*)nullptr);
+    return hipGetLastError();
+}
+
+// Softmax and greedy argmax of the same x in the softmax's three passes
+// (the slice maxima carry their first indices).  x must not alias y.
+hipError_t launch_softmax_argmax_ws(const float* x, float* y, uint32_t N, float* ws, uint32_t* index_out,
+                                    hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    if (N < kSmxMultiMin || !ws) {
+        hipError_t e = launch_argmax(x, N, index_out, s);
+        if (e != hipSuccess) return e;
+        return launch_softmax(x, y, N, s);
+    }
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    uint32_t* first = reinterpret_cast<uint32_t*>(ws + 2 * G + 8);
+    hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, first);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws, x, (const uint32_t*)first, index_out);
     return hipGetLastError();
 }
 

@@ -98,6 +98,11 @@ hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t 
 size_t softmax_workspace_bytes(uint32_t N);
 size_t argmax_workspace_bytes(uint32_t N);
 hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hipStream_t s);
+// Softmax of x into y and the greedy argmax of x into *index_out (device),
+// in the softmax's passes when N is large enough for its multi-workgroup
+// form; ws as for launch_softmax_ws; x must not alias y.
+hipError_t launch_softmax_argmax_ws(const float* x, float* y, uint32_t N, float* ws, uint32_t* index_out,
+                                    hipStream_t s);
 hipError_t launch_argmax_ws(const float* x, uint32_t N, uint32_t* out, uint32_t* pos_inout, uint32_t* hist,
                             uint32_t* hist_n, uint32_t hist_cap, float* ws, hipStream_t s);
 // C[M x N] (row stride ldc) = A (row stride lda) . B, B[k*ldb + j] or, with

@@ -189,6 +189,42 @@ def test_softmax_multi_workgroup(qa, N):
         assert np.max(np.abs(y[nz] - want[nz]) / want[nz]) <= 2e-6
 
 
+def test_softmax_argmax_fused(qa):
+    """qh_softmax_argmax_f32_ws: the probabilities are bit-identical to
+    qh_softmax_f32_ws and the index is the reference argmax of x (first index
+    of the maximum, NaN never wins, NaN at index 0 gives 0) on the
+    multi-workgroup path and on the small-N path; aliasing is refused."""
+    lib = qa.lib()
+    rng = orc.rng_for(213)
+    cases = []
+    for N in (100, 16384, 128256, 131077):
+        base = (orc.gen_f32(N, rng) * 3).astype(np.float32)
+        cases.append(base)
+        if N >= 16384:
+            tie = base.copy()
+            tie[[N // 7, N // 2, N - 3]] = 50.0
+            nan_mid = base.copy()
+            nan_mid[[3, N // 2]] = np.nan
+            nan_mid[N - 100] = 60.0
+            nan0 = base.copy()
+            nan0[0] = np.nan
+            cases += [tie, nan_mid, nan0, np.zeros(N, np.float32)]
+    for x in cases:
+        N = x.size
+        dx = qa.DeviceBuffer.from_numpy(x)
+        dy, dy2 = qa.DeviceBuffer(N * 4), qa.DeviceBuffer(N * 4)
+        ws = qa.DeviceBuffer(lib.qh_softmax_workspace_bytes(N))
+        out = qa.DeviceBuffer(4)
+        qa.check(lib.qh_softmax_argmax_f32_ws(dx.ptr, dy.ptr, N, out.ptr, ws.ptr, None))
+        qa.check(lib.qh_softmax_f32_ws(dx.ptr, dy2.ptr, N, ws.ptr, None))
+        qa.check(lib.qh_device_synchronize())
+        y, y2 = dy.download(np.float32, (N,)), dy2.download(np.float32, (N,))
+        assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+        assert int(out.download(np.uint32, (1,))[0]) == orc.argmax(x)
+    from qorus_amd import _lib as L
+    assert lib.qh_softmax_argmax_f32_ws(dx.ptr, dx.ptr, N, out.ptr, ws.ptr, None) == L.Q_ERR_ALIASING
+
+
 # ------------------------------------------------------------ fp32 matmul --
 
 def _mat_tensor(qa, arr, ne0, ne1, nb0, nb1=4):
