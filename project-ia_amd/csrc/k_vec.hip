@@ -159,22 +159,51 @@ __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uin
     __shared__ float red[4];
     __shared__ uint32_t redi[4];
     const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    if (!first_idx) {
+        float m = -INFINITY;
+        for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) m = fmaxf(m, x[i]);
+        m = block_max<256>(m, red);
+        if (threadIdx.x == 0) ws[blockIdx.x] = m;
+        return;
+    }
+    // One pass: each thread's (max, first index holding it) over its
+    // elements in increasing index order (NaN never compares greater), then
+    // the larger value or, on equal values, the smaller index.  The value
+    // is the same max as the fmaxf form above.
     float m = -INFINITY;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) m = fmaxf(m, x[i]);
-    m = block_max<256>(m, red);
-    if (threadIdx.x == 0) ws[blockIdx.x] = m;
-    if (!first_idx) return;
     uint32_t f = 0xFFFFFFFFu;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256)
-        if (x[i] == m) {
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
+        const float v = x[i];
+        if (v > m || (f == 0xFFFFFFFFu && v == m)) {
+            m = v;
             f = i;
-            break;
         }
+    }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) f = min(f, (uint32_t)__shfl_xor((int)f, off));
-    if ((threadIdx.x & 63) == 0) redi[threadIdx.x >> 6] = f;
+    for (int off = 32; off > 0; off >>= 1) {
+        const float om = __shfl_xor(m, off);
+        const uint32_t of = (uint32_t)__shfl_xor((int)f, off);
+        if (om > m || (om == m && of < f)) {
+            m = om;
+            f = of;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = m;
+        redi[threadIdx.x >> 6] = f;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) first_idx[blockIdx.x] = min(min(redi[0], redi[1]), min(redi[2], redi[3]));
+    if (threadIdx.x == 0) {
+        m = red[0];
+        f = redi[0];
+        for (int w = 1; w < 4; ++w)
+            if (red[w] > m || (red[w] == m && redi[w] < f)) {
+                m = red[w];
+                f = redi[w];
+            }
+        ws[blockIdx.x] = m;
+        first_idx[blockIdx.x] = f;
+    }
 }
 
 __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint32_t N, uint32_t slice, uint32_t G,
@@ -210,17 +239,26 @@ __global__ __launch_bounds__(256) void k_smx_norm(float* y, uint32_t N, uint32_t
                                                   const float* ws, const float* x, const uint32_t* first_idx,
                                                   uint32_t* index_out) {
     __shared__ float inv_s;
-    if (index_out && blockIdx.x == 0 && threadIdx.x == 0) {
+    __shared__ float red[4];
+    __shared__ uint32_t redi[4];
+    if (index_out && blockIdx.x == 0) {
+        // slices are in index order: the smallest first index among the
+        // slices holding the global max is the first index overall
         float m = -INFINITY;
-        for (uint32_t g = 0; g < G; ++g) m = fmaxf(m, ws[g]);
-        uint32_t best = 0;
-        for (uint32_t g = 0; g < G; ++g)
-            if (ws[g] == m && first_idx[g] != 0xFFFFFFFFu) {
-                best = first_idx[g];
-                break;
-            }
-        if (x[0] != x[0]) best = 0;
-        *index_out = best;
+        for (uint32_t g = threadIdx.x; g < G; g += 256) m = fmaxf(m, ws[g]);
+        m = block_max<256>(m, red);
+        uint32_t best = 0xFFFFFFFFu;
+        for (uint32_t g = threadIdx.x; g < G; g += 256)
+            if (ws[g] == m && first_idx[g] < best) best = first_idx[g];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) best = min(best, (uint32_t)__shfl_xor((int)best, off));
+        if ((threadIdx.x & 63) == 0) redi[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            best = min(min(redi[0], redi[1]), min(redi[2], redi[3]));
+            if (best == 0xFFFFFFFFu || x[0] != x[0]) best = 0;
+            *index_out = best;
+        }
     }
     if (threadIdx.x == 0) {
         float total = 0.0f;
