@@ -206,12 +206,44 @@ __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uin
     }
 }
 
+// With index_out: workgroup 0 also writes the greedy argmax of x (reference
+// src/main.c:870-881: first index of the maximum, strict >, index 0 when
+// x[0] is NaN or nothing compares greater) from the slice maxima and their
+// first indices, loaded with the maxima (slices are in index order: the
+// smallest first index among the slices holding the global max is the first
+// index overall).
 __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint32_t N, uint32_t slice, uint32_t G,
-                                                 float* ws) {
+                                                 float* ws, const uint32_t* first_idx, uint32_t* index_out) {
     __shared__ float red[4];
+    __shared__ uint32_t redi[4];
+    constexpr int kPerThread = (kSmxMaxSlices + 255) / 256;
+    const bool arg = index_out && blockIdx.x == 0;
+    float wv[kPerThread];
+    uint32_t fv[kPerThread];
     float m = -INFINITY;
-    for (uint32_t g = threadIdx.x; g < G; g += 256) m = fmaxf(m, ws[g]);
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+        const uint32_t g = threadIdx.x + 256u * k;
+        wv[k] = g < G ? ws[g] : -INFINITY;
+        fv[k] = (arg && g < G) ? first_idx[g] : 0xFFFFFFFFu;
+        m = fmaxf(m, wv[k]);
+    }
     m = block_max<256>(m, red);
+    if (arg) {
+        uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k)
+            if (wv[k] == m && fv[k] < best) best = fv[k];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) best = min(best, (uint32_t)__shfl_xor((int)best, off));
+        if ((threadIdx.x & 63) == 0) redi[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            best = min(min(redi[0], redi[1]), min(redi[2], redi[3]));
+            if (best == 0xFFFFFFFFu || x[0] != x[0]) best = 0;
+            *index_out = best;
+        }
+    }
     const uint32_t nv = N & ~7u;
     const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
     float ls = 0.0f;
@@ -231,35 +263,9 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
     if (threadIdx.x == 0) ws[G + blockIdx.x] = sum;
 }
 
-// With index_out: block 0 also writes the greedy argmax of x (reference
-// src/main.c:870-881: first index of the maximum, strict >, index 0 when
-// x[0] is NaN or nothing compares greater) from the slice maxima and their
-// first indices.
 __global__ __launch_bounds__(256) void k_smx_norm(float* y, uint32_t N, uint32_t slice, uint32_t G,
-                                                  const float* ws, const float* x, const uint32_t* first_idx,
-                                                  uint32_t* index_out) {
+                                                  const float* ws) {
     __shared__ float inv_s;
-    __shared__ float red[4];
-    __shared__ uint32_t redi[4];
-    if (index_out && blockIdx.x == 0) {
-        // slices are in index order: the smallest first index among the
-        // slices holding the global max is the first index overall
-        float m = -INFINITY;
-        for (uint32_t g = threadIdx.x; g < G; g += 256) m = fmaxf(m, ws[g]);
-        m = block_max<256>(m, red);
-        uint32_t best = 0xFFFFFFFFu;
-        for (uint32_t g = threadIdx.x; g < G; g += 256)
-            if (ws[g] == m && first_idx[g] < best) best = first_idx[g];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) best = min(best, (uint32_t)__shfl_xor((int)best, off));
-        if ((threadIdx.x & 63) == 0) redi[threadIdx.x >> 6] = best;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            best = min(min(redi[0], redi[1]), min(redi[2], redi[3]));
-            if (best == 0xFFFFFFFFu || x[0] != x[0]) best = 0;
-            *index_out = best;
-        }
-    }
     if (threadIdx.x == 0) {
         float total = 0.0f;
         for (uint32_t g = 0; g < G; ++g) total = total + ws[G + g];
@@ -291,9 +297,9 @@ hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hi
     uint32_t sl, G;
     smx_shape(N, &sl, &G);
     hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, (uint32_t*)nullptr);
-    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws);
-    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws, x, (const uint32_t*)nullptr,
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const uint32_t*)nullptr,
                        (uint32_t*)nullptr);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
     return hipGetLastError();
 }
 
@@ -311,8 +317,8 @@ hipError_t launch_softmax_argmax_ws(const float* x, float* y, uint32_t N, float*
     smx_shape(N, &sl, &G);
     uint32_t* first = reinterpret_cast<uint32_t*>(ws + 2 * G + 8);
     hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, first);
-    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws);
-    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws, x, (const uint32_t*)first, index_out);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const uint32_t*)first, index_out);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
     return hipGetLastError();
 }
 
