@@ -74,7 +74,7 @@ q_error_code q_sample_token(const float* __restrict__ logits, uint32_t vocab_siz
         float* dl = static_cast<float*>(buf);
         uint32_t* di = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(buf) + (((size_t)V * 4 + 255) & ~(size_t)255));
         QH_TRY(hipMemcpyAsync(dl, logits, (size_t)V * 4, hipMemcpyHostToDevice, d->stream));
-        QH_TRY(launch_argmax(dl, V, di, d->stream));
+        QH_TRY(launch_argmax_ws(dl, V, di, nullptr, nullptr, nullptr, 0, d->reduce_ws, d->stream));
         QH_TRY(hipMemcpyAsync(token_id_out, di, 4, hipMemcpyDeviceToHost, d->stream));
         QH_TRY(hipStreamSynchronize(d->stream));
         return Q_OK;

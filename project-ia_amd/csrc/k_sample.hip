@@ -105,13 +105,49 @@ __global__ __launch_bounds__(kThreads) void k_exp_elems(const float* __restrict_
     }
 }
 
-// One wave.  Blocks of 512 elements (64 groups of 8) are staged through
+// One wave; lanes 0..7 carry the eight sums.  out[0] = 1/sum.
+// Sparse form (nz = nzc[0] nonzero terms, listed in index order in nzl, at
+// most kSparseTerms): only the nonzero terms are added, each to its lane's
+// sum in index order.  Adding a zero to a sum that starts at +0 never
+// changes it, so this is the dense sum to the bit.
+// Dense form: blocks of 512 elements (64 groups of 8) are staged through
 // LDS, the next block's global loads issued before the current block is
-// summed; lanes 0..7 carry the eight sums.  out[0] = 1/sum.
-__global__ __launch_bounds__(64) void k_lane_sums(const float* __restrict__ e, uint32_t V, float* __restrict__ out) {
+// summed.
+constexpr uint32_t kSparseTerms = 4096;
+
+__global__ __launch_bounds__(64) void k_lane_sums(const float* __restrict__ e, uint32_t V,
+                                                const uint32_t* __restrict__ nzl, const uint32_t* __restrict__ nzc,
+                                                float* __restrict__ out) {
     __shared__ float blk[2][512];
     const uint32_t lane = threadIdx.x;
     const uint32_t nv = V & ~7u, ng = nv / 8;  // groups of 8 in the vector part
+    const uint32_t nz = nzc[0];
+    if (nz <= kSparseTerms) {
+        float acc = 0.0f;
+        for (uint32_t b = 0; b < nz; b += 64) {
+            const uint32_t j = b + lane;
+            const uint32_t id = j < nz ? nzl[j] : 0u;
+            const float v = j < nz ? e[id] : 0.0f;
+            const uint32_t m = nz - b < 64 ? nz - b : 64;
+            for (uint32_t u = 0; u < m; ++u) {
+                const uint32_t i = (uint32_t)__shfl((int)id, (int)u);
+                const float ev = __shfl(v, (int)u);
+                if (i < nv && (i & 7u) == lane) acc = acc + ev;
+            }
+        }
+        float sl[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sl[l] = __shfl(acc, l);
+        float sum = ((sl[0] + sl[4]) + (sl[1] + sl[5])) + ((sl[2] + sl[6]) + (sl[3] + sl[7]));
+        // tail terms (index >= nv) close the list, at most 7 of them
+        const uint32_t t0 = nz > 7 ? nz - 7 : 0;
+        for (uint32_t j = t0; j < nz; ++j) {
+            const uint32_t i = nzl[j];
+            if (i >= nv) sum = sum + e[i];
+        }
+        if (lane == 0) out[0] = 1.0f / sum;
+        return;
+    }
     const uint32_t nb = (ng + 63) / 64;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
     auto load = [&](uint32_t k) {
@@ -219,7 +255,8 @@ __global__ __launch_bounds__(64) void k_sorted_walk(const uint32_t* __restrict__
 }
 
 // Valid tokens with nonzero p, in index order (list), their count and the
-// last valid index: three parallel passes over chunks of kChunk elements
+// last valid index (a null mask: every token valid): three parallel passes
+// over chunks of kChunk elements
 // (thread t of a chunk owns elements 4t .. 4t+3, so thread order is index
 // order).  k_count: per-chunk count and last valid index + 1;
 // k_scan_chunks (one workgroup): exclusive offsets, total, last valid;
@@ -233,7 +270,7 @@ __device__ __forceinline__ uint32_t take4(const float* p, const uint8_t* m, uint
 #pragma unroll
     for (uint32_t u = 0; u < 4; ++u) {
         const uint32_t i = i0 + u;
-        const bool valid = i < V && m[i] != 0;
+        const bool valid = i < V && (!m || m[i] != 0);
         if (valid) last1 = i + 1;
         if (valid && p[i] != 0.0f) {
             bits |= 1u << u;
@@ -436,7 +473,8 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
     uint32_t* list = reinterpret_cast<uint32_t*>(W + L.list);
     uint32_t* chunks = reinterpret_cast<uint32_t*>(W + L.chunks);
     float* smx = reinterpret_cast<float*>(W + L.smx);
-    float* scal = reinterpret_cast<float*>(W + L.scal);  // [0,1] top-k walk, [2,3] top-p walk, [4,5] compact, [6] 1/sum
+    float* scal = reinterpret_cast<float*>(W + L.scal);  // [0,1] top-k walk, [2,3] top-p walk, [4,5] compact,
+                                                         // [6] 1/sum, [8,9] nonzero exponentials
     void* sort_tmp = W + L.sort_tmp;
     const dim3 grid((V + kThreads - 1) / kThreads);
 #define QH_K(...)                                   \
@@ -453,7 +491,12 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
         const uint32_t G = (V + kMaxSlice - 1) / kMaxSlice;
         QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, scaled, V, smx);
         QH_K(k_exp_elems, grid, dim3(kThreads), 0, s, scaled, V, smx, G, probs);
-        QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, probs, V, scal + 6);
+        const uint32_t nch = (V + kChunk - 1) / kChunk;
+        uint32_t* nzc = reinterpret_cast<uint32_t*>(scal + 8);
+        QH_K(k_count, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, nch);
+        QH_K(k_scan_chunks, dim3(1), dim3(kThreads), 0, s, chunks, nch, nzc);
+        QH_K(k_scatter, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, list);
+        QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, probs, V, (const uint32_t*)list, (const uint32_t*)nzc, scal + 6);
         QH_K(k_scale_by, grid, dim3(kThreads), 0, s, probs, V, scal + 6);
     }
     auto sort_desc = [&](void) -> hipError_t {
