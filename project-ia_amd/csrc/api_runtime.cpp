@@ -65,6 +65,23 @@ q_error_code stage(Device* d, int slot, size_t bytes, void** out) {
     return Q_OK;
 }
 
+q_error_code h2d_pinned(Device* d, void* dst, const void* src, size_t bytes) {
+    if (d->host_stage_bytes < bytes) {
+        if (d->host_stage) {
+            QH_TRY(hipStreamSynchronize(d->stream));
+            QH_TRY(hipHostFree(d->host_stage));
+            d->host_stage = nullptr;
+            d->host_stage_bytes = 0;
+        }
+        const size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        QH_TRY(hipHostMalloc(&d->host_stage, want, hipHostMallocDefault));
+        d->host_stage_bytes = want;
+    }
+    std::memcpy(d->host_stage, src, bytes);
+    QH_TRY(hipMemcpyAsync(dst, d->host_stage, bytes, hipMemcpyHostToDevice, d->stream));
+    return Q_OK;
+}
+
 // ---- q_context side table ----
 static std::mutex g_ctx_mu;
 static std::map<const q_context*, CtxState*> g_ctx;

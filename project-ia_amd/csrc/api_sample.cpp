@@ -73,7 +73,7 @@ q_error_code q_sample_token(const float* __restrict__ logits, uint32_t vocab_siz
         QH_TRY_CODE(stage(d, 1, (size_t)V * 4 + 256, &buf));
         float* dl = static_cast<float*>(buf);
         uint32_t* di = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(buf) + (((size_t)V * 4 + 255) & ~(size_t)255));
-        QH_TRY(hipMemcpyAsync(dl, logits, (size_t)V * 4, hipMemcpyHostToDevice, d->stream));
+        QH_TRY_CODE(h2d_pinned(d, dl, logits, (size_t)V * 4));
         QH_TRY(launch_argmax_ws(dl, V, di, nullptr, nullptr, nullptr, 0, d->reduce_ws, d->stream));
         QH_TRY(hipMemcpyAsync(token_id_out, di, 4, hipMemcpyDeviceToHost, d->stream));
         QH_TRY(hipStreamSynchronize(d->stream));
@@ -112,7 +112,7 @@ q_error_code q_sample_token(const float* __restrict__ logits, uint32_t vocab_siz
     uint8_t* B = static_cast<uint8_t*>(buf);
     float* dl = reinterpret_cast<float*>(B);
     uint32_t* dt = reinterpret_cast<uint32_t*>(B + lb);
-    QH_TRY(hipMemcpyAsync(dl, logits, (size_t)V * 4, hipMemcpyHostToDevice, d->stream));
+    QH_TRY_CODE(h2d_pinned(d, dl, logits, (size_t)V * 4));
     QH_TRY(launch_sample(dl, sp, B + lb + 256, dt, d->stream));
     QH_TRY(hipMemcpyAsync(token_id_out, dt, 4, hipMemcpyDeviceToHost, d->stream));
     QH_TRY(hipStreamSynchronize(d->stream));

@@ -65,6 +65,7 @@ struct ModelPlan {
     hipGraphExec_t gen_graph = nullptr;      // decode step + greedy feedback + pos advance
     void* sample_ws = nullptr;               // device workspace of sampled generation
     uint32_t* pinned = nullptr;              // host staging for token/pos
+    float* pinned_logits = nullptr;          // host staging for the logits llama_forward returns
 };
 
 static std::mutex g_plan_mu;
@@ -79,6 +80,7 @@ void plan_destroy(CtxState* st) {
     if (p->arena) (void)hipFree(p->arena);
     if (p->sample_ws) (void)hipFree(p->sample_ws);
     if (p->pinned) (void)hipHostFree(p->pinned);
+    if (p->pinned_logits) (void)hipHostFree(p->pinned_logits);
     if (p->stream) (void)hipStreamDestroy(p->stream);
     delete p;
     st->plan = nullptr;
@@ -504,6 +506,8 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned_logits), (size_t)cfg.vocab_size * 4, hipHostMallocDefault);
     if (e != hipSuccess) {
         fail(e, "decode plan allocation");
         st->plan = p;
@@ -591,9 +595,12 @@ q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restr
         QH_TRY(hipMemcpyAsync(p->pos, &p->pinned[1], 4, hipMemcpyHostToDevice, p->stream));
         QH_TRY(hipGraphLaunch(p->step_graph, p->stream));
     }
-    QH_TRY(hipMemcpyAsync(logits, p->logits, (size_t)model->config.vocab_size * 4, hipMemcpyDeviceToHost,
+    // through pinned memory (one DMA, then a host copy): a pageable copy of
+    // the 513 KB Llama-3 logits is several times slower
+    QH_TRY(hipMemcpyAsync(p->pinned_logits, p->logits, (size_t)model->config.vocab_size * 4, hipMemcpyDeviceToHost,
                           p->stream));
     QH_TRY(hipStreamSynchronize(p->stream));
+    std::memcpy(logits, p->pinned_logits, (size_t)model->config.vocab_size * 4);
     return Q_OK;
 }
 

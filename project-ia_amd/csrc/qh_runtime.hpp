@@ -40,6 +40,8 @@ struct Device {
     // Grow-only device staging used by the host-pointer entry points.
     void* stage[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t stage_bytes[4] = {0, 0, 0, 0};
+    void* host_stage = nullptr;  // pinned host bounce buffer (hipHostMalloc)
+    size_t host_stage_bytes = 0;
     // Partials of the multi-workgroup softmax/argmax used by the entry points
     // that take no workspace (allocated once at initialization).
     float* reduce_ws = nullptr;
@@ -52,6 +54,10 @@ q_error_code device(Device** out);
 
 // Ensures staging slot `slot` holds at least `bytes`; returns its address.
 q_error_code stage(Device* d, int slot, size_t bytes, void** out);
+// Host -> device copy of `bytes` from pageable host memory through the
+// device's pinned bounce buffer (a host memcpy, then one DMA on d->stream).
+// The caller holds d->mu and synchronizes d->stream before the next use.
+q_error_code h2d_pinned(Device* d, void* dst, const void* src, size_t bytes);
 
 // HBM mirror of a q_context (side table keyed by the context address).
 struct CtxState {
