@@ -9,28 +9,26 @@
 //      order, or for V < 8 the sampler's own scalar fallback (expf,
 //      sequential sum, multiply by 1/sum, uniform if the sum is not
 //      positive);
-//   3. top-k (0 < k < V): the k largest p (stable descending radix sort of
-//      (p, index): equal probabilities keep index order), their sum taken
-//      sequentially in that order, p_i /= sum inside the set, 0 outside;
-//      k >= V: every token valid, p unchanged;
-//   4. top-p (0 < top_p < 1): stable descending sort of the current p, the
-//      running fp32 sum in that order until it reaches top_p (the smallest
-//      such prefix; all V if it never does), p_i /= that sum inside the
-//      prefix, 0 outside; top_p >= 1: every token valid (this replaces a
-//      top-k set, as in the reference);
+//   3. top-k (0 < k < V): the k largest p (equal probabilities in index
+//      order), their sum taken sequentially in that order, p_i /= sum inside
+//      the set, 0 outside; k >= V: every token valid, p unchanged;
+//   4. top-p (0 < top_p < 1): the current p in descending order (ties in
+//      index order), the running fp32 sum in that order until it reaches
+//      top_p (the smallest such prefix; all V if it never does), p_i /= that
+//      sum inside the prefix, 0 outside; top_p >= 1: every token valid (this
+//      replaces a top-k set, as in the reference);
 //   5. the token: running fp32 sum over the valid tokens in index order,
 //      the first with r < sum; past the end, the last valid token.
-// The sequential fp32 sums (3, 4, 5) run in one wave, element by element
-// in the reference's order; zeros are skipped where adding them cannot
-// change the sum (x + 0 == x), so the chains cover only nonzero entries.
+// Steps 3-5 run in one workgroup (k_filter_draw) on the nonzero
+// probabilities only: the reference's clamped polynomial exp makes all but a
+// few exactly zero, and a zero is never selected before a nonzero value,
+// never changes a running sum and is never drawn.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
-
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include "qh_kernels.hpp"
 #include "qh_sample.hpp"
@@ -185,75 +183,6 @@ __global__ __launch_bounds__(kThreads) void k_scale_by(float* __restrict__ p, ui
     if (i < V) p[i] = p[i] * s;
 }
 
-// Sort keys: the bit pattern of p (p >= 0 orders as an unsigned integer;
-// -0.0 is folded onto +0.0 so that all zeros tie), values: the index.
-__global__ __launch_bounds__(kThreads) void k_keys(const float* __restrict__ p, uint32_t V, uint32_t* __restrict__ keys,
-                                                 uint32_t* __restrict__ idx) {
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < V) {
-        const uint32_t b = __float_as_uint(p[i]);
-        keys[i] = b == 0x80000000u ? 0u : b;
-        idx[i] = i;
-    }
-}
-
-__global__ __launch_bounds__(kThreads) void k_fill_u8(uint8_t* __restrict__ m, uint32_t V, uint8_t v) {
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < V) m[i] = v;
-}
-
-// mask[idx[j]] = 1 for j < n, n = *n_dev when n_dev is given, else n_host.
-__global__ __launch_bounds__(kThreads) void k_mark(const uint32_t* __restrict__ idx, uint32_t n_host,
-                                                 const uint32_t* __restrict__ n_dev, uint8_t* __restrict__ m) {
-    const uint32_t n = n_dev ? *n_dev : n_host;
-    const uint32_t j = blockIdx.x * kThreads + threadIdx.x;
-    if (j < n) m[idx[j]] = 1;
-}
-
-// p_i = mask_i ? p_i / s : 0 when s > 0 (the reference leaves p alone
-// otherwise).
-__global__ __launch_bounds__(kThreads) void k_renorm(float* __restrict__ p, const uint8_t* __restrict__ m, uint32_t V,
-                                                   const float* __restrict__ s_dev) {
-    const float s = *s_dev;
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < V && s > 0.0f) p[i] = m[i] ? p[i] / s : 0.0f;
-}
-
-// One wave walks the sorted keys (descending p) in order with a running fp32
-// sum: the sum of the first n entries (n = limit), or, with a threshold
-// (top_p), the first prefix whose sum reaches it.  The walk stops at the
-// first zero key: every later entry is zero and cannot change the sum.
-//   out[0] = the sum, out[1] (as u32) = the prefix length (limit if the
-//   threshold is never reached).
-__global__ __launch_bounds__(64) void k_sorted_walk(const uint32_t* __restrict__ keys, uint32_t limit, float threshold,
-                                                  bool use_threshold, float* __restrict__ out) {
-    const uint32_t lane = threadIdx.x;
-    float sum = 0.0f;
-    uint32_t cut = limit;
-    bool done = false;
-    for (uint32_t base = 0; base < limit && !done; base += 64) {
-        const uint32_t j = base + lane;
-        const float v = j < limit ? __uint_as_float(keys[j]) : 0.0f;
-        const uint64_t nz = __ballot(v != 0.0f && j < limit);
-        const uint32_t n = (uint32_t)__popcll(nz);
-        // Entries past the first zero are zero (sorted descending): the
-        // nonzero ones of this batch are its first n lanes.
-        for (uint32_t u = 0; u < n; ++u) {
-            sum += __shfl(v, (int)u);
-            if (use_threshold && sum >= threshold) {
-                cut = base + u + 1;
-                done = true;
-                break;
-            }
-        }
-        if (n < 64) done = true;
-    }
-    if (lane == 0) {
-        out[0] = sum;
-        out[1] = __uint_as_float(cut);
-    }
-}
-
 // Valid tokens with nonzero p, in index order (list), their count and the
 // last valid index (a null mask: every token valid): three parallel passes
 // over chunks of kChunk elements
@@ -369,31 +298,256 @@ __global__ __launch_bounds__(kThreads) void k_scatter(const float* __restrict__ 
         if (bits & (1u << u)) list[at++] = i0 + u;
 }
 
-// The token: running fp32 sum over list (index order), first with r < sum;
-// otherwise the last valid index, or V - 1 when none is valid.
-__global__ __launch_bounds__(64) void k_pick(const float* __restrict__ p, const uint32_t* __restrict__ list,
-                                           const uint32_t* __restrict__ cnt, uint32_t V, float r,
-                                           uint32_t* __restrict__ token) {
-    const uint32_t lane = threadIdx.x;
-    const uint32_t n = cnt[0], last1 = cnt[1];
+// Selection and draw, one workgroup (steps 3-5).  The nonzero p, in index
+// order, are loaded as (index, p) entries (from the nonzero-exponential list,
+// or from every index when there is none); a zero p is never selected and
+// never drawn, so only these entries are sorted and walked.  Sorting uses
+// 64-bit keys (p bits << 32 | ~position): descending order is p descending,
+// equal p in index order.  Zero-valued tokens enter a top-k set only as its
+// last members (lowest indices first); they change no sum, and they matter
+// only as the fallback "last valid index", which is computed from their
+// count.  Up to kSelLds entries live in LDS; more (near-flat distributions)
+// run the same code on global scratch.
+constexpr uint32_t kSelThreads = 1024;
+constexpr uint32_t kSelLds = 4096;
+
+struct FilterArgs {
+    const float* p;
+    uint32_t V;
+    const uint32_t* cand;    // nonzero-exponential indices in index order, or null: 0..V-1
+    const uint32_t* cand_n;  // their count
+    uint32_t top_k;
+    float top_p;
+    uint32_t nucleus_all;
+    float r;
+    unsigned long long* gkeys;  // >= pow2(V) entries (large path)
+    float* gq;                  // V
+    uint32_t* gidx;             // V
+    uint8_t* gvalid;            // V
+    uint32_t* token;
+};
+
+constexpr uint32_t kNotReached = 0xFFFFFFFFu;
+
+__device__ __forceinline__ uint32_t key_pos(unsigned long long k) { return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull); }
+
+// Descending bitonic sort of n (a power of two) keys by the whole workgroup.
+__device__ void bitonic_desc(unsigned long long* k, uint32_t n) {
+    for (uint32_t size = 2; size <= n; size <<= 1)
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = threadIdx.x; t < n / 2; t += kSelThreads) {
+                const uint32_t i = (t / stride) * 2u * stride + (t % stride), l = i + stride;
+                const unsigned long long x = k[i], y = k[l];
+                const bool desc = (i & size) == 0;
+                if (desc ? (x < y) : (x > y)) {
+                    k[i] = y;
+                    k[l] = x;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// Keys of the entries with a nonzero value (others and the padding up to
+// np: 0), then the sort.
+__device__ void sort_nonzero(unsigned long long* K, const float* Q, uint32_t n, uint32_t np) {
+    for (uint32_t pos = threadIdx.x; pos < np; pos += kSelThreads) {
+        unsigned long long key = 0;
+        if (pos < n) {
+            const uint32_t b = __float_as_uint(Q[pos]);
+            if ((b & 0x7FFFFFFFu) != 0u) key = ((unsigned long long)b << 32) | (0xFFFFFFFFu - pos);
+        }
+        K[pos] = key;
+    }
+    __syncthreads();
+    bitonic_desc(K, np);
+}
+
+// Wave 0: running fp32 sum over the sorted entries in order (the first
+// `limit`; the walk ends at the first zero key), with a threshold: the
+// first prefix reaching it.  Results in *sum_out, *cut_out (the prefix
+// length, or kNotReached).
+__device__ void walk_sorted(const unsigned long long* K, const float* Q, uint32_t limit, float thr, bool use_thr,
+                            float* sum_out, uint32_t* cut_out) {
+    const uint32_t lane = threadIdx.x & 63;
     float sum = 0.0f;
-    uint32_t tok = last1 ? last1 - 1u : V - 1u;
+    uint32_t cut = kNotReached;
     bool done = false;
-    for (uint32_t base = 0; base < n && !done; base += 64) {
+    for (uint32_t base = 0; base < limit && !done; base += 64) {
         const uint32_t j = base + lane;
-        const uint32_t id = j < n ? list[j] : 0u;
-        const float v = j < n ? p[id] : 0.0f;
-        const uint32_t m = n - base < 64 ? n - base : 64;
-        for (uint32_t u = 0; u < m; ++u) {
-            sum += __shfl(v, (int)u);
-            if (r < sum) {
-                tok = (uint32_t)__shfl((int)id, (int)u);
+        const unsigned long long key = j < limit ? K[j] : 0ull;
+        const float q = key ? Q[key_pos(key)] : 0.0f;
+        const uint32_t nb = (uint32_t)__popcll(__ballot(key != 0ull));
+        for (uint32_t u = 0; u < nb; ++u) {
+            sum += __shfl(q, (int)u);
+            if (use_thr && sum >= thr) {
+                cut = base + u + 1;
                 done = true;
                 break;
             }
         }
+        if (nb < 64) done = true;
     }
-    if (lane == 0) *token = tok;
+    if (lane == 0) {
+        *sum_out = sum;
+        *cut_out = cut;
+    }
+}
+
+__global__ __launch_bounds__(kSelThreads) void k_filter_draw(FilterArgs a) {
+    __shared__ unsigned long long s_keys[kSelLds];
+    __shared__ float s_q[kSelLds];
+    __shared__ uint32_t s_idx[kSelLds];
+    __shared__ uint8_t s_valid[kSelLds];
+    __shared__ uint32_t s_wcnt[kSelThreads / 64];
+    __shared__ uint32_t s_red[kSelThreads / 64];
+    __shared__ float s_sum;
+    __shared__ uint32_t s_cut;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t V = a.V;
+    const uint32_t nc = a.cand ? *a.cand_n : V;
+    const bool big = nc > kSelLds;
+    unsigned long long* K = big ? a.gkeys : s_keys;
+    float* Q = big ? a.gq : s_q;
+    uint32_t* I = big ? a.gidx : s_idx;
+    uint8_t* VAL = big ? a.gvalid : s_valid;
+
+    // nonzero entries in index order
+    uint32_t n = 0;
+    for (uint32_t base = 0; base < nc; base += kSelThreads) {
+        const uint32_t j = base + tid;
+        uint32_t i = 0;
+        float v = 0.0f;
+        bool take = false;
+        if (j < nc) {
+            i = a.cand ? a.cand[j] : j;
+            v = a.p[i];
+            take = (__float_as_uint(v) & 0x7FFFFFFFu) != 0u;
+        }
+        const uint64_t bal = __ballot(take);
+        const uint32_t below = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) s_wcnt[wave] = (uint32_t)__popcll(bal);
+        __syncthreads();
+        uint32_t off = n, tot = 0;
+        for (uint32_t w = 0; w < kSelThreads / 64; ++w) {
+            if (w < wave) off += s_wcnt[w];
+            tot += s_wcnt[w];
+        }
+        if (take) {
+            I[off + below] = i;
+            Q[off + below] = v;
+        }
+        n += tot;
+        __syncthreads();
+    }
+    uint32_t np = 1;
+    while (np < n) np <<= 1;
+
+    // max index over the entries marked valid (all threads; result in s_red[0])
+    auto max_valid_index = [&](void) -> uint32_t {
+        uint32_t mx = 0;
+        for (uint32_t pos = tid; pos < n; pos += kSelThreads)
+            if (VAL[pos] && I[pos] > mx) mx = I[pos];
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint32_t t = (uint32_t)__shfl_xor((int)mx, o);
+            mx = t > mx ? t : mx;
+        }
+        if (lane == 0) s_red[wave] = mx;
+        __syncthreads();
+        uint32_t r = 0;
+        for (uint32_t w = 0; w < kSelThreads / 64; ++w) r = s_red[w] > r ? s_red[w] : r;
+        __syncthreads();
+        return r;
+    };
+    auto renorm = [&](float sum, bool all) {
+        if (sum > 0.0f)
+            for (uint32_t pos = tid; pos < n; pos += kSelThreads) Q[pos] = (all || VAL[pos]) ? Q[pos] / sum : 0.0f;
+        __syncthreads();
+    };
+
+    bool all_valid = false, filtered = false;
+    uint32_t last = 0;
+    // top-k (reference main.c:431-521)
+    if (a.top_k > 0) {
+        if (a.top_k >= V) {
+            all_valid = true;
+        } else {
+            sort_nonzero(K, Q, n, np);
+            const uint32_t kk = a.top_k < n ? a.top_k : n;
+            if (wave == 0) walk_sorted(K, Q, kk, 0.0f, false, &s_sum, &s_cut);
+            for (uint32_t pos = tid; pos < n; pos += kSelThreads) VAL[pos] = 0;
+            __syncthreads();
+            for (uint32_t j = tid; j < kk; j += kSelThreads) VAL[key_pos(K[j])] = 1;
+            __syncthreads();
+            last = max_valid_index();
+            if (a.top_k > n) {
+                // the (top_k - n)-th zero-valued index: the nonzero indices
+                // at or below the candidate push it up by one each
+                if (tid == 0) {
+                    uint32_t c = a.top_k - n - 1u;
+                    for (uint32_t pos = 0; pos < n && I[pos] <= c; ++pos) ++c;
+                    s_cut = c;
+                }
+                __syncthreads();
+                last = s_cut > last ? s_cut : last;
+            }
+            renorm(s_sum, false);
+            all_valid = false;
+        }
+        filtered = true;
+    }
+    // top-p (reference main.c:720-808, 525-597)
+    if (a.top_p > 0.0f) {
+        if (a.top_p >= 1.0f) {
+            all_valid = true;
+        } else {
+            sort_nonzero(K, Q, n, np);
+            if (wave == 0) walk_sorted(K, Q, n, a.top_p, a.nucleus_all == 0u, &s_sum, &s_cut);
+            __syncthreads();
+            const float sum = s_sum;
+            const uint32_t cut = s_cut;
+            if (a.nucleus_all || cut == kNotReached) {
+                // never reached (or not searched): the nucleus is every token
+                all_valid = true;
+                renorm(sum, true);
+            } else {
+                for (uint32_t pos = tid; pos < n; pos += kSelThreads) VAL[pos] = 0;
+                __syncthreads();
+                for (uint32_t j = tid; j < cut; j += kSelThreads) VAL[key_pos(K[j])] = 1;
+                __syncthreads();
+                last = max_valid_index();
+                renorm(sum, false);
+                all_valid = false;
+            }
+        }
+        filtered = true;
+    }
+    if (!filtered) all_valid = true;
+    if (all_valid) last = V - 1u;
+    // the draw (reference main.c:811-849): running sum over the valid
+    // entries in index order
+    if (wave == 0) {
+        float cs = 0.0f;
+        uint32_t tok = last;
+        bool done = false;
+        for (uint32_t base = 0; base < n && !done; base += 64) {
+            const uint32_t j = base + lane;
+            const bool ok = j < n && (all_valid || VAL[j]);
+            const float q = ok ? Q[j] : 0.0f;
+            const uint32_t id = j < n ? I[j] : 0u;
+            const uint32_t m = n - base < 64 ? n - base : 64;
+            for (uint32_t u = 0; u < m; ++u) {
+                if (!__shfl((int)ok, (int)u)) continue;
+                cs += __shfl(q, (int)u);
+                if (a.r < cs) {
+                    tok = (uint32_t)__shfl((int)id, (int)u);
+                    done = true;
+                    break;
+                }
+            }
+        }
+        if (lane == 0) *a.token = tok;
+    }
 }
 
 // Generation feedback after a sampled token: append it to the history and
@@ -410,36 +564,31 @@ __global__ void k_feedback(const uint32_t* __restrict__ tok, uint32_t* __restric
 inline size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct Layout {
-    size_t scaled, probs, keys, idx, keys2, idx2, mask, list, chunks, smx, scal, sort_tmp, total;
-    size_t sort_bytes;
+    size_t scaled, probs, list, chunks, smx, scal, gkeys, gq, gidx, gvalid, total;
 };
 
-hipError_t layout_of(uint32_t V, Layout* L) {
-    size_t tmp = 0;
-    hipError_t e = rocprim::radix_sort_pairs_desc(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                                  (const uint32_t*)nullptr, (uint32_t*)nullptr, V, 0, 32);
-    if (e != hipSuccess) return e;
+Layout layout_of(uint32_t V) {
+    Layout L{};
     size_t at = 0;
     auto carve = [&](size_t b) {
         const size_t o = at;
         at += up256(b);
         return o;
     };
-    L->scaled = carve((size_t)V * 4);
-    L->probs = carve((size_t)V * 4);
-    L->keys = carve((size_t)V * 4);
-    L->idx = carve((size_t)V * 4);
-    L->keys2 = carve((size_t)V * 4);
-    L->idx2 = carve((size_t)V * 4);
-    L->mask = carve(V);
-    L->list = carve((size_t)V * 4);
-    L->chunks = carve((size_t)2 * ((V + kChunk - 1) / kChunk) * 4);
-    L->smx = carve((size_t)((V + kMaxSlice - 1) / kMaxSlice) * 4);
-    L->scal = carve(64);
-    L->sort_bytes = tmp;
-    L->sort_tmp = carve(tmp ? tmp : 1);
-    L->total = at;
-    return hipSuccess;
+    size_t p2 = 1;
+    while (p2 < V) p2 <<= 1;
+    L.scaled = carve((size_t)V * 4);
+    L.probs = carve((size_t)V * 4);
+    L.list = carve((size_t)V * 4);
+    L.chunks = carve((size_t)2 * ((V + kChunk - 1) / kChunk) * 4);
+    L.smx = carve((size_t)((V + kMaxSlice - 1) / kMaxSlice) * 4);
+    L.scal = carve(64);
+    L.gkeys = carve(p2 * 8);
+    L.gq = carve((size_t)V * 4);
+    L.gidx = carve((size_t)V * 4);
+    L.gvalid = carve(V);
+    L.total = at;
+    return L;
 }
 
 }  // namespace
@@ -450,43 +599,35 @@ hipError_t launch_token_feedback(const uint32_t* tok, uint32_t* pos, uint32_t* h
     return hipGetLastError();
 }
 
-size_t sample_workspace_bytes(uint32_t V) {
-    Layout L{};
-    if (V == 0 || layout_of(V, &L) != hipSuccess) return 0;
-    return L.total;
-}
+size_t sample_workspace_bytes(uint32_t V) { return V == 0 ? 0 : layout_of(V).total; }
 
 hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, uint32_t* token, hipStream_t s) {
     const uint32_t V = sp.vocab;
     if (V == 0 || !logits || !ws || !token) return hipErrorInvalidValue;
-    Layout L{};
-    hipError_t e = layout_of(V, &L);
-    if (e != hipSuccess) return e;
+    const Layout L = layout_of(V);
     uint8_t* W = static_cast<uint8_t*>(ws);
     float* scaled = reinterpret_cast<float*>(W + L.scaled);
     float* probs = reinterpret_cast<float*>(W + L.probs);
-    uint32_t* keys = reinterpret_cast<uint32_t*>(W + L.keys);
-    uint32_t* idx = reinterpret_cast<uint32_t*>(W + L.idx);
-    uint32_t* keys2 = reinterpret_cast<uint32_t*>(W + L.keys2);
-    uint32_t* idx2 = reinterpret_cast<uint32_t*>(W + L.idx2);
-    uint8_t* mask = W + L.mask;
     uint32_t* list = reinterpret_cast<uint32_t*>(W + L.list);
     uint32_t* chunks = reinterpret_cast<uint32_t*>(W + L.chunks);
     float* smx = reinterpret_cast<float*>(W + L.smx);
-    float* scal = reinterpret_cast<float*>(W + L.scal);  // [0,1] top-k walk, [2,3] top-p walk, [4,5] compact,
-                                                         // [6] 1/sum, [8,9] nonzero exponentials
-    void* sort_tmp = W + L.sort_tmp;
+    float* scal = reinterpret_cast<float*>(W + L.scal);  // [6] 1/sum, [8,9] nonzero exponentials
     const dim3 grid((V + kThreads - 1) / kThreads);
-#define QH_K(...)                                   \
-    do {                                            \
-        hipLaunchKernelGGL(__VA_ARGS__);            \
+    hipError_t e;
+#define QH_K(...)                                            \
+    do {                                                     \
+        hipLaunchKernelGGL(__VA_ARGS__);                     \
         if ((e = hipGetLastError()) != hipSuccess) return e; \
     } while (0)
 
-    // 1-2: temperature and softmax
+    // 1-2: temperature and softmax; the nonzero exponentials are listed in
+    // index order for the sums and the selection
     QH_K(k_scale_temp, grid, dim3(kThreads), 0, s, logits, V, sp.n_mul, sp.inv_temperature, sp.temperature, scaled);
+    FilterArgs fa{};
     if (V < 8) {
         QH_K(k_softmax_small, dim3(1), dim3(64), 0, s, scaled, V, probs);
+        fa.cand = nullptr;
+        fa.cand_n = nullptr;
     } else {
         const uint32_t G = (V + kMaxSlice - 1) / kMaxSlice;
         QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, scaled, V, smx);
@@ -498,52 +639,22 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
         QH_K(k_scatter, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, list);
         QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, probs, V, (const uint32_t*)list, (const uint32_t*)nzc, scal + 6);
         QH_K(k_scale_by, grid, dim3(kThreads), 0, s, probs, V, scal + 6);
+        fa.cand = list;
+        fa.cand_n = nzc;
     }
-    auto sort_desc = [&](void) -> hipError_t {
-        size_t tb = L.sort_bytes;
-        QH_K(k_keys, grid, dim3(kThreads), 0, s, probs, V, keys, idx);
-        return rocprim::radix_sort_pairs_desc(sort_tmp, tb, static_cast<const uint32_t*>(keys), keys2,
-                                              static_cast<const uint32_t*>(idx), idx2, V, 0, 32, s);
-    };
-    bool mask_set = false;
-    // 3: top-k
-    if (sp.top_k > 0) {
-        if (sp.top_k >= V) {
-            QH_K(k_fill_u8, grid, dim3(kThreads), 0, s, mask, V, (uint8_t)1);
-        } else {
-            if ((e = sort_desc()) != hipSuccess) return e;
-            QH_K(k_sorted_walk, dim3(1), dim3(64), 0, s, keys2, sp.top_k, 0.0f, false, scal);
-            QH_K(k_fill_u8, grid, dim3(kThreads), 0, s, mask, V, (uint8_t)0);
-            QH_K(k_mark, dim3((sp.top_k + kThreads - 1) / kThreads), dim3(kThreads), 0, s, idx2, sp.top_k,
-                 (const uint32_t*)nullptr, mask);
-            QH_K(k_renorm, grid, dim3(kThreads), 0, s, probs, mask, V, scal);
-        }
-        mask_set = true;
-    }
-    // 4: top-p
-    if (sp.top_p > 0.0f) {
-        if (sp.top_p >= 1.0f) {
-            QH_K(k_fill_u8, grid, dim3(kThreads), 0, s, mask, V, (uint8_t)1);
-        } else {
-            if ((e = sort_desc()) != hipSuccess) return e;
-            // nucleus_all: the reference's prefix-sum buffer could not be
-            // allocated; its search then keeps every token.
-            QH_K(k_sorted_walk, dim3(1), dim3(64), 0, s, keys2, V, sp.top_p, !sp.nucleus_all, scal + 2);
-            QH_K(k_fill_u8, grid, dim3(kThreads), 0, s, mask, V, (uint8_t)0);
-            QH_K(k_mark, grid, dim3(kThreads), 0, s, idx2, V, reinterpret_cast<const uint32_t*>(scal + 3), mask);
-            QH_K(k_renorm, grid, dim3(kThreads), 0, s, probs, mask, V, scal + 2);
-        }
-        mask_set = true;
-    }
-    // Neither filter: every token valid.
-    if (!mask_set) QH_K(k_fill_u8, grid, dim3(kThreads), 0, s, mask, V, (uint8_t)1);
-    // 5: the token
-    uint32_t* cnt = reinterpret_cast<uint32_t*>(scal + 4);
-    const uint32_t nchunks = (V + kChunk - 1) / kChunk;
-    QH_K(k_count, dim3(nchunks), dim3(kThreads), 0, s, probs, mask, V, chunks, nchunks);
-    QH_K(k_scan_chunks, dim3(1), dim3(kThreads), 0, s, chunks, nchunks, cnt);
-    QH_K(k_scatter, dim3(nchunks), dim3(kThreads), 0, s, probs, mask, V, chunks, list);
-    QH_K(k_pick, dim3(1), dim3(64), 0, s, probs, list, cnt, V, sp.r, token);
+    // 3-5: top-k, top-p, the draw
+    fa.p = probs;
+    fa.V = V;
+    fa.top_k = sp.top_k;
+    fa.top_p = sp.top_p;
+    fa.nucleus_all = sp.nucleus_all ? 1u : 0u;
+    fa.r = sp.r;
+    fa.gkeys = reinterpret_cast<unsigned long long*>(W + L.gkeys);
+    fa.gq = reinterpret_cast<float*>(W + L.gq);
+    fa.gidx = reinterpret_cast<uint32_t*>(W + L.gidx);
+    fa.gvalid = W + L.gvalid;
+    fa.token = token;
+    QH_K(k_filter_draw, dim3(1), dim3(kSelThreads), 0, s, fa);
 #undef QH_K
     return hipSuccess;
 }
