@@ -154,6 +154,20 @@ hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s) {
 // [2G+8, 3G+8) the slices' first max indices (fused argmax).
 // With first_idx: also the first index of the slice holding its maximum
 // (0xFFFFFFFF when no element equals it, e.g. an all-NaN slice).
+// A thread's elements of a slice are base, base + 256, ... < b1; they are
+// loaded kSmxUnroll at a time, all loads issued before any value is used
+// (one memory round trip per chunk instead of one per element).
+constexpr int kSmxUnroll = kSmxSlice / 256;
+
+__device__ __forceinline__ void load_slice_chunk(const float* x, uint32_t base, uint32_t b1,
+                                                 float (&v)[kSmxUnroll]) {
+#pragma unroll
+    for (int u = 0; u < kSmxUnroll; ++u) {
+        const uint32_t i = base + 256u * u;
+        v[u] = i < b1 ? x[i] : 0.0f;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uint32_t slice, float* ws,
                                                  uint32_t* first_idx) {
     __shared__ float red[4];
@@ -161,7 +175,13 @@ __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uin
     const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
     if (!first_idx) {
         float m = -INFINITY;
-        for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) m = fmaxf(m, x[i]);
+        for (uint32_t base = b0 + threadIdx.x; base < b1; base += 256u * kSmxUnroll) {
+            float v[kSmxUnroll];
+            load_slice_chunk(x, base, b1, v);
+#pragma unroll
+            for (int u = 0; u < kSmxUnroll; ++u)
+                if (base + 256u * u < b1) m = fmaxf(m, v[u]);
+        }
         m = block_max<256>(m, red);
         if (threadIdx.x == 0) ws[blockIdx.x] = m;
         return;
@@ -172,11 +192,16 @@ __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uin
     // is the same max as the fmaxf form above.
     float m = -INFINITY;
     uint32_t f = 0xFFFFFFFFu;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
-        const float v = x[i];
-        if (v > m || (f == 0xFFFFFFFFu && v == m)) {
-            m = v;
-            f = i;
+    for (uint32_t base = b0 + threadIdx.x; base < b1; base += 256u * kSmxUnroll) {
+        float v[kSmxUnroll];
+        load_slice_chunk(x, base, b1, v);
+#pragma unroll
+        for (int u = 0; u < kSmxUnroll; ++u) {
+            const uint32_t i = base + 256u * u;
+            if (i < b1 && (v[u] > m || (f == 0xFFFFFFFFu && v[u] == m))) {
+                m = v[u];
+                f = i;
+            }
         }
     }
 #pragma unroll
@@ -218,6 +243,11 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
     __shared__ uint32_t redi[4];
     constexpr int kPerThread = (kSmxMaxSlices + 255) / 256;
     const bool arg = index_out && blockIdx.x == 0;
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    // The slice's first chunk does not depend on the max: load it first.
+    uint32_t base = b0 + threadIdx.x;
+    float xv[kSmxUnroll];
+    load_slice_chunk(x, base, b1, xv);
     float wv[kPerThread];
     uint32_t fv[kPerThread];
     float m = -INFINITY;
@@ -245,19 +275,26 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
         }
     }
     const uint32_t nv = N & ~7u;
-    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
     float ls = 0.0f;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
-        const float d = x[i] - m;
-        if (i < nv) {
-            const float e = exp_approx(d);
-            ls = ls + e;
-            y[i] = e;
-        } else {
-            const float e = expf(d);
-            y[i] = e;
-            ws[2 * G + (i - nv)] = e;
+    while (base < b1) {
+#pragma unroll
+        for (int u = 0; u < kSmxUnroll; ++u) {
+            const uint32_t i = base + 256u * u;
+            if (i < b1) {
+                const float d = xv[u] - m;
+                if (i < nv) {
+                    const float e = exp_approx(d);
+                    ls = ls + e;
+                    y[i] = e;
+                } else {
+                    const float e = expf(d);
+                    y[i] = e;
+                    ws[2 * G + (i - nv)] = e;
+                }
+            }
         }
+        base += 256u * kSmxUnroll;
+        if (base < b1) load_slice_chunk(x, base, b1, xv);
     }
     const float sum = block_sum<256>(ls, red);
     if (threadIdx.x == 0) ws[G + blockIdx.x] = sum;
@@ -266,16 +303,47 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
 __global__ __launch_bounds__(256) void k_smx_norm(float* y, uint32_t N, uint32_t slice, uint32_t G,
                                                   const float* ws) {
     __shared__ float inv_s;
-    if (threadIdx.x == 0) {
+    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
+    uint32_t base = b0 + threadIdx.x;
+    float yv[kSmxUnroll];
+    load_slice_chunk(y, base, b1, yv);
+    // total = slice sums in slice order, then the tail values in index order
+    // (sequential adds).  Wave 0 loads them in parallel, lane l holding
+    // entries l, l + 64, ...; the adds read them back lane by lane.
+    if (threadIdx.x < 64) {
+        constexpr int kPer = kSmxMaxSlices / 64;
+        const uint32_t ln = threadIdx.x, nt = N - (N & ~7u);
+        float pv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t g = (uint32_t)k * 64u + ln;
+            pv[k] = g < G ? ws[G + g] : 0.0f;
+        }
+        const float tv = ln < nt ? ws[2 * G + ln] : 0.0f;
         float total = 0.0f;
-        for (uint32_t g = 0; g < G; ++g) total = total + ws[G + g];
-        for (uint32_t i = (N & ~7u); i < N; ++i) total = total + ws[2 * G + (i - (N & ~7u))];
-        inv_s = 1.0f / total;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t g0 = (uint32_t)k * 64u;
+            if (g0 < G) {
+                const uint32_t n = min(64u, G - g0);
+                for (uint32_t l = 0; l < n; ++l)
+                    total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv[k]), (int)l));
+            }
+        }
+        for (uint32_t l = 0; l < nt; ++l) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tv), (int)l));
+        if (ln == 0) inv_s = 1.0f / total;
     }
     __syncthreads();
     const float inv = inv_s;
-    const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) y[i] = y[i] * inv;
+    while (base < b1) {
+#pragma unroll
+        for (int u = 0; u < kSmxUnroll; ++u) {
+            const uint32_t i = base + 256u * u;
+            if (i < b1) y[i] = yv[u] * inv;
+        }
+        base += 256u * kSmxUnroll;
+        if (base < b1) load_slice_chunk(y, base, b1, yv);
+    }
 }
 
 static void smx_shape(uint32_t N, uint32_t* slice, uint32_t* G) {
@@ -431,11 +499,16 @@ __global__ __launch_bounds__(256) void k_amax_part(const float* __restrict__ x, 
     const uint32_t b0 = blockIdx.x * slice, b1 = min(N, b0 + slice);
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
-        const float v = x[i];
-        if (arg_better(v, i, bv, bi)) {
-            bv = v;
-            bi = i;
+    for (uint32_t base = b0 + threadIdx.x; base < b1; base += 256u * kSmxUnroll) {
+        float v[kSmxUnroll];
+        load_slice_chunk(x, base, b1, v);
+#pragma unroll
+        for (int u = 0; u < kSmxUnroll; ++u) {
+            const uint32_t i = base + 256u * u;
+            if (i < b1 && arg_better(v[u], i, bv, bi)) {
+                bv = v[u];
+                bi = i;
+            }
         }
     }
 #pragma unroll
