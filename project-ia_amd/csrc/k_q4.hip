@@ -271,7 +271,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     // and conversion stay inside the wave (no workgroup barrier, digits go
     // straight to registers).
     constexpr bool kWaveLocal = J == 1 && G == 1;
-    constexpr int kPass = XF ? (kMaxBlk + kThreads - 1) / kThreads : 0;
+    constexpr int kQPass = XF ? (4 * kMaxBlk + kThreads - 1) / kThreads : 0;
     constexpr int kLd = XF ? (kWaveLocal ? 8 : (kMaxBlk * 8 + kThreads - 1) / kThreads) : 0;
     constexpr int kXs = 36;
     constexpr int kLds = !XF ? 1 : (kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
@@ -355,29 +355,36 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             zz[0] = ok[0] ? __uint_as_float(o[6].y) : 0.0f;
             return;
         }
-        float xv[kPass > 0 ? kPass : 1][32];
+        // Four threads per block (a lane quad), thread 4c+i taking elements
+        // 8i..8i+7 of block c and making dword i of its planes, so every
+        // wave shares the conversion.
+        float xv[kQPass > 0 ? kQPass : 1][8];
 #pragma unroll
-        for (int ps = 0; ps < kPass; ++ps) {
-            const uint32_t c = (uint32_t)(ps * kThreads) + threadIdx.x;
+        for (int ps = 0; ps < kQPass; ++ps) {
+            const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
+            const uint32_t c = t >> 2, qi = t & 3u;
             const uint32_t cc = c < (uint32_t)kMaxBlk ? c : 0u;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const v4u32 v = *reinterpret_cast<const v4u32*>(xs + cc * kXs + (uint32_t)i * 4u);
-                xv[ps][4 * i] = __uint_as_float(v[0]);
-                xv[ps][4 * i + 1] = __uint_as_float(v[1]);
-                xv[ps][4 * i + 2] = __uint_as_float(v[2]);
-                xv[ps][4 * i + 3] = __uint_as_float(v[3]);
+            for (int h = 0; h < 2; ++h) {
+                const v4u32 v = *reinterpret_cast<const v4u32*>(xs + cc * kXs + qi * 8u + (uint32_t)h * 4u);
+                xv[ps][4 * h] = __uint_as_float(v[0]);
+                xv[ps][4 * h + 1] = __uint_as_float(v[1]);
+                xv[ps][4 * h + 2] = __uint_as_float(v[2]);
+                xv[ps][4 * h + 3] = __uint_as_float(v[3]);
             }
         }
         __syncthreads();  // the planes overwrite the staged x
+        uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
 #pragma unroll
-        for (int ps = 0; ps < kPass; ++ps) {
-            const uint32_t c = (uint32_t)(ps * kThreads) + threadIdx.x;
+        for (int ps = 0; ps < kQPass; ++ps) {
+            const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
+            const uint32_t c = t >> 2, qi = t & 3u;
+            uint32_t pl[6], kq, zq;
+            prep_quarter(xv[ps], pl, kq, zq);  // whole quads share c, so they agree on c < kMaxBlk
             if (c < (uint32_t)kMaxBlk) {
-                uint4 o[7];
-                prep_block(xv[ps], o);
 #pragma unroll
-                for (int p = 0; p < 7; ++p) lds[p * kMaxBlk + c] = o[p];
+                for (int p = 0; p < 6; ++p) ldw[((uint32_t)p * kMaxBlk + c) * 4u + qi] = pl[p];
+                ldw[(6u * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : 0u);
             }
         }
         __syncthreads();

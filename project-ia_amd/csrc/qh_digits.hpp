@@ -122,6 +122,53 @@ __device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[7]
     out[6] = make_uint4((uint32_t)k, __float_as_uint(bad ? __builtin_nanf("") : 0.0f), 0u, 0u);
 }
 
+// prep_block split over the 4 lanes of an aligned lane quad: lane i of the
+// quad holds elements 8i..8i+7 of the block in v and gets dword i of every
+// plane (pl[p], already XORed with 0x88888888) and the block's (k, z) word
+// pair.  The block maximum is combined across the quad, so all 4 lanes must
+// call it together; the digits are those of prep_block bit for bit.
+__device__ __forceinline__ void prep_quarter(const float (&v)[8], uint32_t (&pl)[6], uint32_t& k_out,
+                                             uint32_t& z_out) {
+    uint32_t mb = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mb = __builtin_elementwise_max(mb, __float_as_uint(v[e]) << 1);
+    mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 1));
+    mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 2));
+    const bool bad = mb >= 0xFF000000u;
+    const float m = __uint_as_float(mb >> 1);
+    int k = 0;
+    if (!bad && m > 0.0f) {
+        const int E = __builtin_amdgcn_frexp_expf(m);  // m < 2^E
+        k = 23 - E;
+        if (rintf(ldexpf(m, k)) > (float)kDigitMax) k -= 1;
+    }
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {
+        const float a0 = bad ? 0.0f : v[2 * pr], a1 = bad ? 0.0f : v[2 * pr + 1];
+        const uint32_t u0 = (uint32_t)((int)rintf(ldexpf(a0, k)) + (int)kDigitBias);
+        const uint32_t u1 = (uint32_t)((int)rintf(ldexpf(a1, k)) + (int)kDigitBias);
+        lo[pr] = (u0 & 0x0F0F0F0Fu) | ((u1 << 4) & 0xF0F0F0F0u);
+        hi[pr] = ((u0 >> 4) & 0x0F0F0F0Fu) | (u1 & 0xF0F0F0F0u);
+    }
+    const uint32_t tl01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x05010400u);
+    const uint32_t tl23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x05010400u);
+    const uint32_t sl01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x00000602u);
+    const uint32_t sl23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x00000602u);
+    const uint32_t th01 = __builtin_amdgcn_perm(hi[1], hi[0], 0x05010400u);
+    const uint32_t th23 = __builtin_amdgcn_perm(hi[3], hi[2], 0x05010400u);
+    const uint32_t sh01 = __builtin_amdgcn_perm(hi[1], hi[0], 0x00000602u);
+    const uint32_t sh23 = __builtin_amdgcn_perm(hi[3], hi[2], 0x00000602u);
+    pl[0] = __builtin_amdgcn_perm(tl23, tl01, 0x05040100u) ^ 0x88888888u;
+    pl[2] = __builtin_amdgcn_perm(tl23, tl01, 0x07060302u) ^ 0x88888888u;
+    pl[4] = __builtin_amdgcn_perm(sl23, sl01, 0x05040100u) ^ 0x88888888u;
+    pl[1] = __builtin_amdgcn_perm(th23, th01, 0x05040100u) ^ 0x88888888u;
+    pl[3] = __builtin_amdgcn_perm(th23, th01, 0x07060302u) ^ 0x88888888u;
+    pl[5] = __builtin_amdgcn_perm(sh23, sh01, 0x05040100u) ^ 0x88888888u;
+    k_out = (uint32_t)k;
+    z_out = __float_as_uint(bad ? __builtin_nanf("") : 0.0f);
+}
+
 // Integer dots of R*J blocks (already loaded) against the x digit planes,
 // accumulated into acc[0..R): plane by plane across all blocks, each plane a
 // 4-deep dot8 chain of its own, planes combined by P = (P << 4) + S_p, so
