@@ -260,21 +260,22 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         coff[j] = cols[j] * 20u;
     }
     // fp32 input: x is loaded with coalesced 16-byte loads before the first
-    // tiles' weight loads (so the conversion waits for x only), staged in
-    // LDS at a 36-float stride per block (conflict-free 16-byte reads), and
-    // thread t then converts blocks t, t + 64*W*G, ... into digit planes in
-    // the same LDS space.
+    // tiles' weight loads (so the conversion waits for x only).  Each lane
+    // quad of the workgroup converts one block at a time straight from its
+    // registers (thread 4c+i: elements 8i..8i+7 of block c) and writes the
+    // digit planes to LDS, from which every lane takes its own columns.
     constexpr int kMaxBlk = 64 * J * W;
     constexpr int kThreads = 64 * W * G;
     // One block column per lane and one wave group (J == 1, G == 1): each
-    // wave converts exactly the 64 blocks its own lanes consume, so staging
-    // and conversion stay inside the wave (no workgroup barrier, digits go
-    // straight to registers).
+    // wave converts exactly the 64 blocks its own lanes consume, one per
+    // lane, staged through LDS at a 36-float stride per block (conflict-free
+    // 16-byte reads); staging and conversion stay inside the wave (no
+    // workgroup barrier, digits go straight to registers).
     constexpr bool kWaveLocal = J == 1 && G == 1;
     constexpr int kQPass = XF ? (4 * kMaxBlk + kThreads - 1) / kThreads : 0;
-    constexpr int kLd = XF ? (kWaveLocal ? 8 : (kMaxBlk * 8 + kThreads - 1) / kThreads) : 0;
+    constexpr int kLd = XF ? (kWaveLocal ? 8 : 2 * kQPass) : 0;
     constexpr int kXs = 36;
-    constexpr int kLds = !XF ? 1 : (kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
+    constexpr int kLds = !XF ? 1 : (kWaveLocal && kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
     __shared__ uint4 lds[kLds];
     __shared__ float lds_ss[XF ? W * G : 1];
     v4u32 xl[kLd > 0 ? kLd : 1], wl[kLd > 0 ? kLd : 1];
@@ -285,7 +286,8 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             __builtin_amdgcn_make_buffer_rsrc((void*)a.xnorm_w, 0, a.xnorm_w ? (int)(a.nblk * 128u) : 0, kBufFlags);
 #pragma unroll
         for (int i = 0; i < kLd; ++i) {
-            const uint32_t f = kWaveLocal ? (uint32_t)(kw * 512 + i * 64 + lane) : (uint32_t)(i * kThreads) + threadIdx.x;
+            const uint32_t f = kWaveLocal ? (uint32_t)(kw * 512 + i * 64 + lane)
+                                          : 2u * ((uint32_t)(i >> 1) * kThreads + threadIdx.x) + (uint32_t)(i & 1);
             xl[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, f * 16u, 0, 0);
             wl[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, f * 16u, 0, 0);
         }
@@ -299,45 +301,94 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     // over the waves in order, so every wave of every workgroup gets the
     // same factor newton(rsqrt(sum/N + eps)) (reference rmsnorm.c:62-71).
     auto convert_x = [&]() {
-        float* xs = reinterpret_cast<float*>(lds);
         const bool norm = a.xnorm_w != nullptr;
         float ss = 0.0f;
+        if constexpr (!kWaveLocal) {
+            // Piece i of this thread is elements 8*qi + 4*(i&1) .. +3 of
+            // block c of pass i>>1 (thread 4c+qi of the pass); the lane quad
+            // of block c converts it straight from registers.
+            float xv[kQPass > 0 ? kQPass : 1][8];
 #pragma unroll
-        for (int i = 0; i < kLd; ++i) {
-            const uint32_t f = kWaveLocal ? (uint32_t)(kw * 512 + i * 64 + lane) : (uint32_t)(i * kThreads) + threadIdx.x;
-            v4u32 v = xl[i];
-            float x0 = __uint_as_float(v[0]), x1 = __uint_as_float(v[1]);
-            float x2 = __uint_as_float(v[2]), x3 = __uint_as_float(v[3]);
-            ss = ss + x0 * x0;
-            ss = ss + x1 * x1;
-            ss = ss + x2 * x2;
-            ss = ss + x3 * x3;
-            if (norm) {
-                v[0] = __float_as_uint(x0 * __uint_as_float(wl[i][0]));
-                v[1] = __float_as_uint(x1 * __uint_as_float(wl[i][1]));
-                v[2] = __float_as_uint(x2 * __uint_as_float(wl[i][2]));
-                v[3] = __float_as_uint(x3 * __uint_as_float(wl[i][3]));
+            for (int i = 0; i < kLd; ++i) {
+                float x4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x4[e] = __uint_as_float(xl[i][e]);
+                    ss = ss + x4[e] * x4[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[i >> 1][4 * (i & 1) + e] = norm ? x4[e] * __uint_as_float(wl[i][e]) : x4[e];
             }
-            if (f < (uint32_t)kMaxBlk * 8u) *reinterpret_cast<v4u32*>(xs + (f >> 3) * kXs + (f & 7u) * 4u) = v;
-        }
-        if (norm) {
+            if (norm) {
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-            if (lane == 0) lds_ss[wave] = ss;
-        }
-        // Wave-local staging needs no barrier: a wave's LDS writes and the
-        // reads that follow them are ordered (the norm's cross-wave sum is
-        // the only workgroup-wide step, and norm is uniform).
-        if (!kWaveLocal || norm) __syncthreads();
-        if (norm) {
-            float tot = lds_ss[0];
+                for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+                if (lane == 0) lds_ss[wave] = ss;
+                __syncthreads();
+                float tot = lds_ss[0];
 #pragma unroll
-            for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
-            const float av = tot / (float)(a.nblk * 32u) + a.eps;
-            const float r0 = __builtin_amdgcn_rsqf(av);
-            rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
-        }
-        if constexpr (kWaveLocal) {
+                for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
+                const float av = tot / (float)(a.nblk * 32u) + a.eps;
+                const float r0 = __builtin_amdgcn_rsqf(av);
+                rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
+            }
+            uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
+#pragma unroll
+            for (int ps = 0; ps < kQPass; ++ps) {
+                const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
+                const uint32_t c = t >> 2, qi = t & 3u;
+                uint32_t pl[6], kq, zq;
+                prep_quarter(xv[ps], pl, kq, zq);  // whole quads share c, so they agree on c < kMaxBlk
+                if (c < (uint32_t)kMaxBlk) {
+#pragma unroll
+                    for (int p = 0; p < 6; ++p) ldw[((uint32_t)p * kMaxBlk + c) * 4u + qi] = pl[p];
+                    ldw[(6u * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : 0u);
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+#pragma unroll
+                for (int p = 0; p < 6; ++p) xp[j][p] = lds[p * kMaxBlk + cols[j]];
+                const uint4 m = lds[6 * kMaxBlk + cols[j]];
+                kk[j] = ok[j] ? (int)m.x : 0;
+                zz[j] = ok[j] ? __uint_as_float(m.y) : 0.0f;
+            }
+        } else {
+            // One block per lane, staged through LDS inside the wave.
+            float* xs = reinterpret_cast<float*>(lds);
+#pragma unroll
+            for (int i = 0; i < kLd; ++i) {
+                const uint32_t f = (uint32_t)(kw * 512 + i * 64 + lane);
+                v4u32 v = xl[i];
+                float x0 = __uint_as_float(v[0]), x1 = __uint_as_float(v[1]);
+                float x2 = __uint_as_float(v[2]), x3 = __uint_as_float(v[3]);
+                ss = ss + x0 * x0;
+                ss = ss + x1 * x1;
+                ss = ss + x2 * x2;
+                ss = ss + x3 * x3;
+                if (norm) {
+                    v[0] = __float_as_uint(x0 * __uint_as_float(wl[i][0]));
+                    v[1] = __float_as_uint(x1 * __uint_as_float(wl[i][1]));
+                    v[2] = __float_as_uint(x2 * __uint_as_float(wl[i][2]));
+                    v[3] = __float_as_uint(x3 * __uint_as_float(wl[i][3]));
+                }
+                if (f < (uint32_t)kMaxBlk * 8u) *reinterpret_cast<v4u32*>(xs + (f >> 3) * kXs + (f & 7u) * 4u) = v;
+            }
+            // A wave's LDS writes and the reads that follow them are ordered;
+            // the norm's cross-wave sum is the only workgroup-wide step (norm
+            // is uniform).
+            if (norm) {
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+                if (lane == 0) lds_ss[wave] = ss;
+                __syncthreads();
+                float tot = lds_ss[0];
+#pragma unroll
+                for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
+                const float av = tot / (float)(a.nblk * 32u) + a.eps;
+                const float r0 = __builtin_amdgcn_rsqf(av);
+                rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
+            }
             float xw[32];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -353,48 +404,6 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             for (int p = 0; p < 6; ++p) xp[0][p] = o[p];
             kk[0] = ok[0] ? (int)o[6].x : 0;
             zz[0] = ok[0] ? __uint_as_float(o[6].y) : 0.0f;
-            return;
-        }
-        // Four threads per block (a lane quad), thread 4c+i taking elements
-        // 8i..8i+7 of block c and making dword i of its planes, so every
-        // wave shares the conversion.
-        float xv[kQPass > 0 ? kQPass : 1][8];
-#pragma unroll
-        for (int ps = 0; ps < kQPass; ++ps) {
-            const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
-            const uint32_t c = t >> 2, qi = t & 3u;
-            const uint32_t cc = c < (uint32_t)kMaxBlk ? c : 0u;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const v4u32 v = *reinterpret_cast<const v4u32*>(xs + cc * kXs + qi * 8u + (uint32_t)h * 4u);
-                xv[ps][4 * h] = __uint_as_float(v[0]);
-                xv[ps][4 * h + 1] = __uint_as_float(v[1]);
-                xv[ps][4 * h + 2] = __uint_as_float(v[2]);
-                xv[ps][4 * h + 3] = __uint_as_float(v[3]);
-            }
-        }
-        __syncthreads();  // the planes overwrite the staged x
-        uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
-#pragma unroll
-        for (int ps = 0; ps < kQPass; ++ps) {
-            const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
-            const uint32_t c = t >> 2, qi = t & 3u;
-            uint32_t pl[6], kq, zq;
-            prep_quarter(xv[ps], pl, kq, zq);  // whole quads share c, so they agree on c < kMaxBlk
-            if (c < (uint32_t)kMaxBlk) {
-#pragma unroll
-                for (int p = 0; p < 6; ++p) ldw[((uint32_t)p * kMaxBlk + c) * 4u + qi] = pl[p];
-                ldw[(6u * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : 0u);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-#pragma unroll
-            for (int p = 0; p < 6; ++p) xp[j][p] = lds[p * kMaxBlk + cols[j]];
-            const uint4 m = lds[6 * kMaxBlk + cols[j]];
-            kk[j] = ok[j] ? (int)m.x : 0;
-            zz[j] = ok[j] ? __uint_as_float(m.y) : 0.0f;
         }
     };
 
