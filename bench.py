@@ -366,38 +366,44 @@ def run_lmhead(args):
     def gemv(t):
         qa.check(lib.qh_gemv_q4_f32_multi(ptr_array([t.addr]), None, ys, 1, x.ptr, ws.ptr, s))
 
-    smx_ws = qa.DeviceBuffer(lib.qh_softmax_workspace_bytes(VOCAB))
+    fws = qa.DeviceBuffer(lib.qh_gemv_softmax_workspace_bytes(VOCAB))
 
-    def softmax_argmax():
-        """softmax of the logits and their greedy argmax in the softmax's
-        three passes (results: q_softmax_f32_avx2 and main.c:870-881)."""
-        qa.check(lib.qh_softmax_argmax_f32_ws(logits.ptr, probs.ptr, VOCAB, tok.ptr, smx_ws.ptr, s))
+    def step(t):
+        """LM head + softmax of the logits + their greedy argmax (results:
+        q_gemv_q4_f32_avx2, q_softmax_f32_avx2 and main.c:870-881); the
+        GEMV leaves the argmax's per-workgroup partials, then the softmax's
+        exp and normalize passes (3 launches)."""
+        qa.check(lib.qh_gemv_q4_f32_softmax_argmax(t.addr, x.ptr, logits.ptr, probs.ptr, tok.ptr, fws.ptr, s))
 
-    graphs = []
-    for t in ts:
+    def capture(n):
+        """One graph of n consecutive steps (weight copy i % LM_COPIES), as
+        the config-2 leg runs its steps."""
         qa.check(lib.qh_stream_begin_capture(s))
-        gemv(t)
-        softmax_argmax()
+        for i in range(n):
+            step(ts[i % LM_COPIES])
         g = C.c_void_p()
         qa.check(lib.qh_stream_end_capture(s, C.byref(g)))
-        graphs.append(g.value)
+        return g.value
+
     steps = max(10, args.steps // 4)
-    for i in range(8):
-        qa.check(lib.qh_graph_launch(graphs[i % LM_COPIES], s))
+    graphs = [capture(8), capture(steps)]
+    qa.check(lib.qh_graph_launch(graphs[0], s))
     stream.sync()
+    qa.check(lib.qh_device_synchronize())
     t0 = time.perf_counter()
-    for i in range(steps):
-        qa.check(lib.qh_graph_launch(graphs[i % LM_COPIES], s))
+    qa.check(lib.qh_graph_launch(graphs[1], s))
     stream.sync()
+    qa.check(lib.qh_device_synchronize())
     wall = time.perf_counter() - t0
     # correctness spot check: the device argmax is the host argmax
     lg = logits.download(np.float32, (VOCAB,))
     tk = int(tok.download(np.uint32, (1,))[0])
     ok = tk == int(np.argmax(lg))
-    # stage timings with events (eager launches on the same stream)
-    stages = {"gemv": [], "softmax_argmax": []}
+    # stage timings with events (eager launches on the same stream): the
+    # whole step, and the plain GEMV launch alone for comparison
+    stages = {"gemv": [], "step": []}
     for i in range(16):
-        for name, fn in (("gemv", lambda: gemv(ts[i % LM_COPIES])), ("softmax_argmax", softmax_argmax)):
+        for name, fn in (("gemv", lambda: gemv(ts[i % LM_COPIES])), ("step", lambda: step(ts[i % LM_COPIES]))):
             a, b = qa.Event(), qa.Event()
             a.record(stream)
             fn()
@@ -409,8 +415,9 @@ def run_lmhead(args):
     ms = wall / steps * 1e3
     nbytes = lmhead_bytes()
     cpu = None if args.no_cpu else run_cpu_lmhead()
-    return {"workload": "config3: LM head 128256x4096 Q4_0 GEMV + softmax over 128256 logits + argmax, "
-                        "hipGraph per step, 2 rotated weight copies",
+    return {"workload": "config3: LM head 128256x4096 Q4_0 GEMV + softmax over 128256 logits + argmax "
+                        "(qh_gemv_q4_f32_softmax_argmax: 3 launches), one hipGraph of all timed steps, "
+                        "2 rotated weight copies",
             "ms_per_step": round(ms, 5), "steps": steps, "alg_bytes": nbytes,
             "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -177,6 +177,19 @@ q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, v
 q_error_code qh_softmax_argmax_f32_ws(const float* x, float* output, uint32_t N, uint32_t* index_out,
                                       void* workspace, qh_stream s);
 
+/* LM head + softmax + greedy argmax: logits = W . x (as qh_gemv_q4_f32),
+ * probs = softmax(logits) and *index_out = argmax(logits) (as
+ * qh_softmax_argmax_f32_ws: the same bits and index).  For 2048 < N <= 4096
+ * and M >= 16384 the GEMV also leaves the argmax's per-workgroup partials,
+ * so no separate pass re-reads the logits (3 launches).  workspace holds
+ * qh_gemv_softmax_workspace_bytes(M) device bytes; probs must not alias
+ * logits or x (Q_ERR_ALIASING).  No reference counterpart (the reference's
+ * generation loop runs the LM head inside llama_forward, then
+ * q_softmax_f32_avx2 and the argmax of src/main.c:870-881). */
+size_t qh_gemv_softmax_workspace_bytes(uint32_t M);
+q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, float* logits, float* probs,
+                                           uint32_t* index_out, void* workspace, qh_stream s);
+
 /* ---- Decode on the device ---- */
 
 /* Greedy generation with no host round trip between steps (no reference

@@ -154,6 +154,8 @@ struct GemvArgs {
     float eps;             // (row values are then scaled by the RMSNorm factor)
     const float* xf;       // fp32 input (N = 32*nblk) when the kernel makes the digits itself
     const float* xnorm_w;  // with xf: RMSNorm weight; digits of x*w, rows scaled by the norm factor
+    float* amax;           // AM: per-workgroup greedy-argmax partials of y, values [0, grid) then
+                           // first indices [grid, 2*grid) (as uint32)
 };
 
 // Segment of tile t (tiles of `tile_rows` rows, numbered across segments).
@@ -229,10 +231,14 @@ __device__ __forceinline__ void store_row_pre(const GemvArgs& a, uint32_t sg, ui
 // SW: SwiGLU pair mode (W == 1): tile u holds rows i0..i0+RT/2-1 of w[0]
 // (W_gate) followed by the same rows of w[1] (W_up), i0 = u*RT/2, and stores
 // h[i] = silu(g_i) * u_i (reference silu.c:75-82, mul_fp32.c) to y[0].
-template <int W, int J, int G, int RT, bool XF, bool SW = false>
+// AM (W == 1, one segment, plain store): every workgroup also writes the
+// (largest value, first row holding it) of the rows it stored to a.amax, the
+// greedy argmax's partials (arg_better), so no separate pass re-reads y.
+template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
 __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     static_assert(W == 1 || G == 1, "multi-wave K split runs one tile per workgroup");
     static_assert(!SW || (W == 1 && RT % 2 == 0), "SwiGLU pairs need one wave per group and even tiles");
+    static_assert(!AM || (W == 1 && !SW), "argmax partials are taken in the one-wave store path");
     const int lane = threadIdx.x & 63;
     // The wave index is uniform per wave; readfirstlane makes that visible to
     // the compiler so tile/segment bookkeeping stays scalar (a vector load of
@@ -249,6 +255,8 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     uint32_t coff[J];
     bool ok[J];
     uint4 xp[J][6];
+    float am_v = -INFINITY;  // AM: this lane's best stored row so far
+    uint32_t am_i = 0xFFFFFFFFu;
     int kk[J];
     float zz[J];
     uint32_t cols[J];
@@ -509,6 +517,13 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < RT; ++r) pv = (r == (lane ^ 1)) ? acc[r] : pv;
                 store_row_pre(a, sg, row0 + lane, v, pv, lane & 1, pos, e.res, e.c, e.sn);
+                if constexpr (AM) {
+                    const uint32_t row = row0 + (uint32_t)lane;
+                    if (row < a.M[sg] && arg_better(v, row, am_v, am_i)) {
+                        am_v = v;
+                        am_i = row;
+                    }
+                }
             }
         } else {
             __shared__ float red[W][RT];
@@ -555,6 +570,35 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         finish_tile(u, qb, sb, eb);
         u = un;
+    }
+    if constexpr (AM) {
+        // Every wave reaches this point (the loop only breaks).
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(am_v, off);
+            const uint32_t oi = (uint32_t)__shfl_xor((int)am_i, off);
+            if (arg_better(ov, oi, am_v, am_i)) {
+                am_v = ov;
+                am_i = oi;
+            }
+        }
+        __shared__ float am_sv[G];
+        __shared__ uint32_t am_si[G];
+        if (lane == 0) {
+            am_sv[g] = am_v;
+            am_si[g] = am_i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int k = 1; k < G; ++k)
+                if (arg_better(am_sv[k], am_si[k], am_v, am_i)) {
+                    am_v = am_sv[k];
+                    am_i = am_si[k];
+                }
+            a.amax[blockIdx.x] = am_v;
+            reinterpret_cast<uint32_t*>(a.amax)[gridDim.x + blockIdx.x] = am_i;
+        }
     }
 }
 
@@ -787,20 +831,26 @@ static int num_cu() {
 }
 
 // Persistent grid: as many groups of G tiles as are resident at once.
-template <int W, int J, int G, int RT, bool XF, bool SW = false>
-static hipError_t launch_gemv_p(const GemvArgs& a, uint32_t tiles, hipStream_t s) {
+template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
+static uint32_t gemv_p_grid(uint32_t tiles) {
     static int occ = 0;
     if (occ == 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT, XF, SW>, 64 * W * G, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k_gemv_p<W, J, G, RT, XF, SW, AM>, 64 * W * G, 0) !=
+                hipSuccess ||
             o < 1)
             o = 1;
         occ = o;
     }
     const uint32_t groups = (tiles + G - 1) / G;
     const uint32_t resident = (uint32_t)(occ * num_cu());
-    const uint32_t grid = groups < resident ? groups : resident;
-    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT, XF, SW>), dim3(grid), dim3(64 * W * G), 0, s, a);
+    return groups < resident ? groups : resident;
+}
+
+template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
+static hipError_t launch_gemv_p(const GemvArgs& a, uint32_t tiles, hipStream_t s) {
+    const uint32_t grid = gemv_p_grid<W, J, G, RT, XF, SW, AM>(tiles);
+    hipLaunchKernelGGL((k_gemv_p<W, J, G, RT, XF, SW, AM>), dim3(grid), dim3(64 * W * G), 0, s, a);
     return hipGetLastError();
 }
 
@@ -897,6 +947,36 @@ hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const floa
     hipError_t e = launch_xprep(x, N, nullptr, 0.0f, nullptr, ws, s);
     if (e != hipSuccess) return e;
     return run_gemv<8, 2, 1, 16, 4>(segs, nseg, nblk, ws, s, dec);
+}
+
+// LM-head form of launch_gemv_f32 (one segment, plain store, 2048 < N <=
+// 4096): y = W . x with the optional RMSNorm of x (dec->norm_w), and the
+// greedy argmax's partials of y written to amax (values [0, n), first
+// indices [n, 2n) as uint32), n = *n_part <= cap.  hipErrorNotSupported for
+// other shapes (the caller then takes the separate argmax pass).
+hipError_t launch_gemv_f32_amax(const GemvSeg& seg, uint32_t N, const float* x, const GemvDecode* dec, float* amax,
+                                uint32_t cap, uint32_t* n_part, hipStream_t s) {
+    if (!x || !amax || !n_part || !seg.w || !seg.y || seg.M == 0) return hipErrorInvalidValue;
+    if (seg.res || seg.hd || seg.rope || (dec && (dec->pos || dec->in_part))) return hipErrorNotSupported;
+    if (N % 32 != 0 || N / 32 <= 64 || N / 32 > 128) return hipErrorNotSupported;
+    constexpr int kRT = 2;
+    GemvArgs a{};
+    a.w[0] = seg.w;
+    a.y[0] = seg.y;
+    a.M[0] = seg.M;
+    const uint32_t tiles = (seg.M + kRT - 1) / kRT;
+    a.tile_end[0] = a.tile_end[1] = a.tile_end[2] = a.tile_end[3] = tiles;
+    a.nseg = 1;
+    a.nblk = N / 32;
+    a.pad = xd_pad(a.nblk);
+    a.xf = x;
+    a.xnorm_w = dec ? dec->norm_w : nullptr;
+    a.eps = dec ? dec->eps : 0.0f;
+    a.amax = amax;
+    const uint32_t grid = gemv_p_grid<1, 2, 4, kRT, true, false, true>(tiles);
+    if (grid > cap) return hipErrorNotSupported;
+    *n_part = grid;
+    return launch_gemv_p<1, 2, 4, kRT, true, false, true>(a, tiles, s);
 }
 
 }  // namespace qh

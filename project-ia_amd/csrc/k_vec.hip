@@ -237,8 +237,11 @@ __global__ __launch_bounds__(256) void k_smx_max(const float* x, uint32_t N, uin
 // first indices, loaded with the maxima (slices are in index order: the
 // smallest first index among the slices holding the global max is the first
 // index overall).
+// The maxima come as Gm partials pmax[0..Gm) (with first indices pfirst for
+// the argmax): the slices' own from k_smx_max, or a producer's.
 __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint32_t N, uint32_t slice, uint32_t G,
-                                                 float* ws, const uint32_t* first_idx, uint32_t* index_out) {
+                                                 float* ws, const float* pmax, const uint32_t* first_idx,
+                                                 uint32_t Gm, uint32_t* index_out) {
     __shared__ float red[4];
     __shared__ uint32_t redi[4];
     constexpr int kPerThread = (kSmxMaxSlices + 255) / 256;
@@ -254,8 +257,8 @@ __global__ __launch_bounds__(256) void k_smx_exp(const float* x, float* y, uint3
 #pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
         const uint32_t g = threadIdx.x + 256u * k;
-        wv[k] = g < G ? ws[g] : -INFINITY;
-        fv[k] = (arg && g < G) ? first_idx[g] : 0xFFFFFFFFu;
+        wv[k] = g < Gm ? pmax[g] : -INFINITY;
+        fv[k] = (arg && g < Gm) ? first_idx[g] : 0xFFFFFFFFu;
         m = fmaxf(m, wv[k]);
     }
     m = block_max<256>(m, red);
@@ -365,8 +368,8 @@ hipError_t launch_softmax_ws(const float* x, float* y, uint32_t N, float* ws, hi
     uint32_t sl, G;
     smx_shape(N, &sl, &G);
     hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, (uint32_t*)nullptr);
-    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const uint32_t*)nullptr,
-                       (uint32_t*)nullptr);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const float*)ws,
+                       (const uint32_t*)nullptr, G, (uint32_t*)nullptr);
     hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
     return hipGetLastError();
 }
@@ -385,7 +388,21 @@ hipError_t launch_softmax_argmax_ws(const float* x, float* y, uint32_t N, float*
     smx_shape(N, &sl, &G);
     uint32_t* first = reinterpret_cast<uint32_t*>(ws + 2 * G + 8);
     hipLaunchKernelGGL(k_smx_max, dim3(G), dim3(256), 0, s, x, N, sl, ws, first);
-    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const uint32_t*)first, index_out);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, (const float*)ws,
+                       (const uint32_t*)first, G, index_out);
+    hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
+    return hipGetLastError();
+}
+
+bool softmax_argmax_takes_parts(uint32_t N) { return N >= kSmxMultiMin; }
+
+hipError_t launch_softmax_argmax_parts(const float* x, float* y, uint32_t N, float* ws, const float* pmax,
+                                       const uint32_t* pfirst, uint32_t Gm, uint32_t* index_out, hipStream_t s) {
+    if (N < kSmxMultiMin || !ws || !pmax || !pfirst || !index_out || Gm == 0 || Gm > kSmxMaxSlices)
+        return hipErrorInvalidValue;
+    uint32_t sl, G;
+    smx_shape(N, &sl, &G);
+    hipLaunchKernelGGL(k_smx_exp, dim3(G), dim3(256), 0, s, x, y, N, sl, G, ws, pmax, pfirst, Gm, index_out);
     hipLaunchKernelGGL(k_smx_norm, dim3(G), dim3(256), 0, s, y, N, sl, G, ws);
     return hipGetLastError();
 }
@@ -406,10 +423,7 @@ hipError_t launch_binary(const float* a, const float* b, float* o, uint32_t N, i
 
 // Greedy argmax (reference src/main.c:870-881): first index of the maximum
 // under strict '>' scanning from index 0; NaN entries never win; a NaN at
-// index 0 makes the answer 0.
-__device__ __forceinline__ bool arg_better(float v, uint32_t i, float bv, uint32_t bi) {
-    return v > bv || (v == bv && i < bi);
-}
+// index 0 makes the answer 0 (arg_better, qh_vec.hpp).
 
 // With pos_inout / hist (the on-device generation loop): also advance the
 // position and append the token to hist[0..hist_cap).
@@ -605,6 +619,15 @@ hipError_t launch_argmax_ws(const float* x, uint32_t N, uint32_t* out, uint32_t*
     smx_shape(N, &sl, &G);
     hipLaunchKernelGGL(k_amax_part, dim3(G), dim3(256), 0, s, x, N, sl, ws);
     hipLaunchKernelGGL(k_amax_final, dim3(1), dim3(256), 0, s, x, N, G, ws, out, pos_inout, hist, hist_n, hist_cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_parts(const float* x, uint32_t N, const float* parts, uint32_t Gm, uint32_t* out,
+                               uint32_t* pos_inout, uint32_t* hist, uint32_t* hist_n, uint32_t hist_cap,
+                               hipStream_t s) {
+    if (!x || N == 0 || !parts || Gm == 0 || !out) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_amax_final, dim3(1), dim3(256), 0, s, x, N, Gm, parts, out, pos_inout, hist, hist_n,
+                       hist_cap);
     return hipGetLastError();
 }
 

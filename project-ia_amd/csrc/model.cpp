@@ -57,6 +57,7 @@ struct ModelPlan {
     uint32_t *tok = nullptr, *pos = nullptr, *hist = nullptr, *hist_n = nullptr;
     uint32_t hist_cap = 0;
     float* amax_ws = nullptr;                // multi-workgroup argmax partials
+    float* amax_parts = nullptr;             // the LM-head GEMV's argmax partials
     bool fused = false;                      // 7-kernel layers (fp32-input GEMVs with fused prologues)
     float* kv = nullptr;
     size_t kv_layer_floats = 0;
@@ -211,9 +212,23 @@ static hipError_t enqueue_step_fused(ModelPlan* p, bool feedback) {
     dn.norm_w = p->out_norm;
     dn.eps = c.rms_norm_eps;
     GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
-    QH_E(launch_gemv_f32(&lm, 1, c.dim, p->x, nullptr, s, &dn));
-    if (feedback)
-        QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap, p->amax_ws, s));
+    // Greedy feedback: the LM-head GEMV also leaves the argmax's partials,
+    // so the argmax is one small combine launch (where the shape allows).
+    uint32_t n_part = 0;
+    const hipError_t ea = feedback ? launch_gemv_f32_amax(lm, c.dim, p->x, &dn, p->amax_parts, kGemvAmaxMaxParts,
+                                                          &n_part, s)
+                                   : hipErrorNotSupported;
+    if (ea == hipSuccess) {
+        QH_E(launch_argmax_parts(p->logits, c.vocab_size, p->amax_parts, n_part, p->tok, p->pos, p->hist, p->hist_n,
+                                 p->hist_cap, s));
+    } else if (ea == hipErrorNotSupported) {
+        QH_E(launch_gemv_f32(&lm, 1, c.dim, p->x, nullptr, s, &dn));
+        if (feedback)
+            QH_E(launch_argmax_ws(p->logits, c.vocab_size, p->tok, p->pos, p->hist, p->hist_n, p->hist_cap,
+                                  p->amax_ws, s));
+    } else {
+        QH_E(ea);
+    }
 #undef QH_E
     return hipSuccess;
 }
@@ -503,6 +518,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     const size_t o_ct = carve(tab * 4), o_st = carve(tab * 4);
     const size_t o_tok = carve(4), o_pos = carve(4), o_hn = carve(4), o_hist = carve((size_t)p->hist_cap * 4);
     const size_t o_aw = carve(argmax_workspace_bytes(cfg.vocab_size));
+    const size_t o_ap = carve((size_t)2 * kGemvAmaxMaxParts * 4);
     hipError_t e = hipMalloc(&p->arena, bytes);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->pinned), 64, hipHostMallocDefault);
@@ -536,6 +552,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     p->hist_n = reinterpret_cast<uint32_t*>(A + o_hn);
     p->hist = reinterpret_cast<uint32_t*>(A + o_hist);
     p->amax_ws = reinterpret_cast<float*>(A + o_aw);
+    p->amax_parts = reinterpret_cast<float*>(A + o_ap);
     p->fused = cfg.dim / 32 <= 128 && cfg.hidden_dim / 32 <= kGemvF32MaxBlk && (p->kvd % 32) == 0;
     st->plan = p;
     st->dev_arena = p->arena;

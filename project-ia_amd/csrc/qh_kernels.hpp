@@ -72,6 +72,14 @@ hipError_t launch_gemv_swiglu(const uint8_t* w_gate, const uint8_t* w_up, uint32
                               const float* norm_w, float eps, float* h, hipStream_t s);
 hipError_t launch_gemv_f32(const GemvSeg* segs, int nseg, uint32_t N, const float* x, uint4* ws,
                            hipStream_t s, const GemvDecode* dec = nullptr);
+// LM-head form (one segment, plain store, 2048 < N <= 4096, optional
+// RMSNorm of x through dec->norm_w): also writes the greedy argmax's
+// partials of y to amax (values [0, n), first indices [n, 2n) as uint32),
+// n = *n_part <= cap, for launch_argmax_parts / launch_softmax_argmax_parts.
+// hipErrorNotSupported for other shapes.
+constexpr uint32_t kGemvAmaxMaxParts = 1024;
+hipError_t launch_gemv_f32_amax(const GemvSeg& seg, uint32_t N, const float* x, const GemvDecode* dec, float* amax,
+                                uint32_t cap, uint32_t* n_part, hipStream_t s);
 
 // ---- batched prefill GEMM (k_gemm.hip) ----
 // Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 or 2) matrices sharing
@@ -105,6 +113,16 @@ hipError_t launch_softmax_argmax_ws(const float* x, float* y, uint32_t N, float*
                                     hipStream_t s);
 hipError_t launch_argmax_ws(const float* x, uint32_t N, uint32_t* out, uint32_t* pos_inout, uint32_t* hist,
                             uint32_t* hist_n, uint32_t hist_cap, float* ws, hipStream_t s);
+// The same two results from Gm precomputed argmax partials (values parts[0,
+// Gm), first indices [Gm, 2Gm) as uint32; launch_gemv_f32_amax): the argmax
+// alone in one launch, or softmax + argmax in two (Gm <= 1024, N large
+// enough for the multi-workgroup softmax; ws as for launch_softmax_ws).
+hipError_t launch_argmax_parts(const float* x, uint32_t N, const float* parts, uint32_t Gm, uint32_t* out,
+                               uint32_t* pos_inout, uint32_t* hist, uint32_t* hist_n, uint32_t hist_cap,
+                               hipStream_t s);
+bool softmax_argmax_takes_parts(uint32_t N);  // N large enough for launch_softmax_argmax_parts
+hipError_t launch_softmax_argmax_parts(const float* x, float* y, uint32_t N, float* ws, const float* pmax,
+                                       const uint32_t* pfirst, uint32_t Gm, uint32_t* index_out, hipStream_t s);
 // C[M x N] (row stride ldc) = A (row stride lda) . B, B[k*ldb + j] or, with
 // bt, B[j*K + k]; reference dot order.
 hipError_t launch_matmul_f32(const float* A, uint32_t lda, const float* B, uint32_t ldb, bool bt, float* C,

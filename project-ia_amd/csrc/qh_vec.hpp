@@ -109,4 +109,12 @@ __device__ __forceinline__ float rms_scale(const float* __restrict__ x, uint32_t
     return r1 * 0.5f;
 }
 
+// Total order of the greedy argmax's candidates (value, index) on non-NaN
+// values: the larger value, on equal values the smaller index; a NaN never
+// wins.  Combining per-subset winners with it gives the first index of the
+// maximum whatever the subsets and their order.
+__device__ __forceinline__ bool arg_better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
 }  // namespace qh

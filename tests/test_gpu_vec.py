@@ -10,6 +10,8 @@ Bars, written out:
     (the polynomial's zeroing is bit-exact; only the sum order differs);
   argmax: identical index, first index on ties.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -223,6 +225,54 @@ def test_softmax_argmax_fused(qa):
         assert int(out.download(np.uint32, (1,))[0]) == orc.argmax(x)
     from qorus_amd import _lib as L
     assert lib.qh_softmax_argmax_f32_ws(dx.ptr, dx.ptr, N, out.ptr, ws.ptr, None) == L.Q_ERR_ALIASING
+
+
+@pytest.mark.parametrize("M,N", [(20000, 4096), (16384, 2080), (5000, 4096), (17000, 1024)])
+def test_gemv_softmax_argmax(qa, M, N):
+    """qh_gemv_q4_f32_softmax_argmax: logits and probabilities bit-identical
+    to qh_gemv_q4_f32_multi followed by qh_softmax_argmax_f32_ws, and the
+    index the reference argmax of the logits, including a three-way tie for
+    the maximum (identical weight rows give identical logits: the first row
+    wins).  The first two shapes take the GEMV's argmax partials, the others
+    the separate passes."""
+    from qorus_amd import _lib as L
+    from qorus_amd import synthetic as syn
+    lib = qa.lib()
+    rng = orc.rng_for(227, M, N)
+    w = syn.gen_q4(M, N, rng)
+    x = syn.gen_f32(N, rng)
+    dw = qa.DeviceBuffer.from_numpy(w)
+    dx = qa.DeviceBuffer.from_numpy(x)
+    W = qa.q4_tensor(dw.ptr, M, N)
+    lg, pr = qa.DeviceBuffer(M * 4), qa.DeviceBuffer(M * 4)
+    lg2, pr2 = qa.DeviceBuffer(M * 4), qa.DeviceBuffer(M * 4)
+    idx, idx2 = qa.DeviceBuffer(4), qa.DeviceBuffer(4)
+    ws = qa.DeviceBuffer(lib.qh_gemv_softmax_workspace_bytes(M))
+    ws2 = qa.DeviceBuffer(lib.qh_softmax_workspace_bytes(M))
+    for tie in (False, True):
+        if tie:
+            # rows 100 and M - 7 become copies of the current maximum's row
+            r = orc.argmax(lg.download(np.float32, (M,)))
+            w[[100, M - 7]] = w[r]
+            dw = qa.DeviceBuffer.from_numpy(w)
+            W = qa.q4_tensor(dw.ptr, M, N)
+        qa.check(lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dx.ptr, lg.ptr, pr.ptr, idx.ptr, ws.ptr, None))
+        ys = (C.c_void_p * 1)(lg2.ptr)
+        Ws = (C.c_void_p * 1)(W.addr)
+        qa.check(lib.qh_gemv_q4_f32_multi(Ws, None, ys, 1, dx.ptr, None, None))
+        qa.check(lib.qh_softmax_argmax_f32_ws(lg2.ptr, pr2.ptr, M, idx2.ptr, ws2.ptr, None))
+        qa.check(lib.qh_device_synchronize())
+        logits = lg.download(np.float32, (M,))
+        assert np.array_equal(bits(logits), bits(lg2.download(np.float32, (M,))))
+        assert np.array_equal(bits(pr.download(np.float32, (M,))), bits(pr2.download(np.float32, (M,))))
+        got = int(idx.download(np.uint32, (1,))[0])
+        assert got == int(idx2.download(np.uint32, (1,))[0]) == orc.argmax(logits)
+        if tie:
+            assert got == min(100, r)
+    assert lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dx.ptr, lg.ptr, lg.ptr, idx.ptr, ws.ptr, None) == \
+        L.Q_ERR_ALIASING
+    assert lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dx.ptr, lg.ptr, pr.ptr, idx.ptr, None, None) == \
+        L.Q_ERR_INVALID_ARG
 
 
 # ------------------------------------------------------------ fp32 matmul --
