@@ -279,10 +279,12 @@ def run_decode(args):
         toks, ms = m.generate(first_tok, DEC_POS, steps)
         # the same decode with each token sampled on the device
         # (temperature 0.8, top-k 40, top-p 0.95)
-        m.upload_kv(kv)
-        m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
-        m.upload_kv(kv)
-        _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
+        ms_s = None
+        if not args.no_sampled_decode:
+            m.upload_kv(kv)
+            m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
+            m.upload_kv(kv)
+            _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
         m.close()
         avg_ctx = DEC_POS + 1 + (steps - 1) / 2
         bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
@@ -295,7 +297,7 @@ def run_decode(args):
                "achieved_GB_s": round(bpt / (ms * 1e-3) / 1e9, 1),
                "frac_of_hbm_peak": round(bpt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
-               "sampled_tok_s": round(1e3 / ms_s, 1),
+               "sampled_tok_s": None if ms_s is None else round(1e3 / ms_s, 1),
                "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
                                    "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
         if not args.no_cpu:
@@ -593,6 +595,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
     ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--decode-warmup", type=int, default=4)
+    ap.add_argument("--no-sampled-decode", action="store_true",
+                    help="config-4 leg: greedy decode only (no device-sampled generation)")
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
     ap.add_argument("--no-lmhead", action="store_true", help="skip the config-3 LM-head leg")
     ap.add_argument("--no-sample", action="store_true", help="skip the q_sample_token leg")
