@@ -58,8 +58,35 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     const uint32_t j0 = chunk * kChunk;
     if (j0 >= S) return;
     __shared__ float smax[4][kMaxGroup];
+    // This workgroup's q rows and each wave's 16 K rows, staged in LDS with
+    // coalesced 16-byte loads (the dot reads them in the reference's
+    // stride-8 element order); K rows padded to kKs floats so that the
+    // stride-8 reads of 8 keys fall in distinct banks.
+    constexpr uint32_t kKs = kHd + 8;
+    constexpr uint32_t kQPieces = group * kHd / 4;
+    __shared__ float s_q[group * kHd];
+    __shared__ float s_k[4][16][kKs];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 3, l = lane & 7;  // key slot g of the pass, reference lane l
+    const float* kbase = kv + (size_t)kvh * head_stride;
+    float4 kr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        // piece pc of the wave's 16 rows: row pc/32, floats 4*(pc%32) ..; keys
+        // past S read row j0 (in bounds) and are masked below
+        const uint32_t pc = (uint32_t)(i * 64 + lane), k = pc >> 5, f = (pc & 31u) * 4u;
+        const uint32_t j = j0 + (uint32_t)wave * 16u + k;
+        kr[i] = *reinterpret_cast<const float4*>(kbase + (size_t)(j < S ? j : j0) * (2 * kHd) + f);
+    }
+    float4 qr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (threadIdx.x < kQPieces) qr = *reinterpret_cast<const float4*>(q + (size_t)kvh * group * kHd + threadIdx.x * 4u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t pc = (uint32_t)(i * 64 + lane), k = pc >> 5, f = (pc & 31u) * 4u;
+        *reinterpret_cast<float4*>(&s_k[wave][k][f]) = kr[i];
+    }
+    if (threadIdx.x < kQPieces) *reinterpret_cast<float4*>(&s_q[threadIdx.x * 4u]) = qr;
+    __syncthreads();
     // q values this lane multiplies: q[h][32t + 8c + l]
     float qv[group][4][4];
 #pragma unroll
@@ -67,23 +94,19 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) qv[h][c][t] = q[(size_t)(kvh * group + h) * kHd + 32 * t + 8 * c + l];
+            for (int t = 0; t < 4; ++t) qv[h][c][t] = s_q[h * kHd + 32 * t + 8 * c + l];
     float mx[group];
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) mx[h] = -INFINITY;
-    const float* kbase = kv + (size_t)kvh * head_stride;
     // 64 keys per workgroup: each wave takes 16 in two passes of 8 (one key
-    // per 8-lane group); both passes' key values are loaded before any use.
+    // per 8-lane group).
     float kk[2][4][4];
 #pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
-        const uint32_t j = j0 + (uint32_t)(wave * 16 + ps * 8 + g);
-        const float* krow = kbase + (size_t)(j < S ? j : 0u) * (2 * kHd);
+    for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) kk[ps][c][t] = krow[32 * t + 8 * c + l];
-    }
+            for (int t = 0; t < 4; ++t) kk[ps][c][t] = s_k[wave][ps * 8 + g][32 * t + 8 * c + l];
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
         const uint32_t j = j0 + (uint32_t)(wave * 16 + ps * 8 + g);
@@ -217,14 +240,16 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
 
 // o = (sum_c o_part[c]) * (1 / sum_c part_sum[c]) (for S < 8, the reference's
 // scalar softmax divides: o = sum / total), then its digits for the Wo GEMV.
-__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ o_part,
+constexpr uint32_t kCombThreads = 64;  // more, smaller workgroups: the combine is one round of loads
+
+__global__ __launch_bounds__(kCombThreads) void k_attn_combine(const float* __restrict__ o_part,
                                                       const float* __restrict__ part_sum,
                                                       const uint32_t* __restrict__ pos_p, uint32_t n_heads,
                                                       uint32_t n_chunks, float* __restrict__ o_out,
                                                       uint32_t pad, uint32_t* __restrict__ xd) {
     const uint32_t S = *pos_p + 1u;
     const uint32_t nch = (S + kChunk - 1) / kChunk;
-    const uint32_t t = blockIdx.x * 256 + threadIdx.x;  // element of o
+    const uint32_t t = blockIdx.x * kCombThreads + threadIdx.x;  // element of o
     const uint32_t N = n_heads * kHd;
     const bool valid = t < N;
     float v = 0.0f;
@@ -276,7 +301,8 @@ static hipError_t run_attention(const AttnArgs& a, hipStream_t s) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t N = a.n_heads * kHd;
-    hipLaunchKernelGGL(k_attn_combine, dim3((N + 255) / 256), dim3(256), 0, s, a.o_part, a.part_sum, a.pos,
+    hipLaunchKernelGGL(k_attn_combine, dim3((N + kCombThreads - 1) / kCombThreads), dim3(kCombThreads), 0, s,
+                       a.o_part, a.part_sum, a.pos,
                        a.n_heads, n_chunks, a.o_out, xd_pad(N / 32), reinterpret_cast<uint32_t*>(a.xd_out));
     return hipGetLastError();
 }

@@ -65,6 +65,26 @@ def test_decode_small_gqa(qa, tmp_path):
         m.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv,P", [(8, 1, 130), (16, 2, 63), (2, 2, 200)])
+def test_decode_gqa_groups(qa, tmp_path, n_heads, n_kv, P):
+    """GQA groups 8 and 1 (the attention kernels are instantiated per group),
+    contexts that end inside a 64-key chunk and on its last key."""
+    h = qa.QorusHeader(vocab=700, dim=128 * n_heads, hidden=1024, n_layers=1, n_heads=n_heads, n_kv=n_kv,
+                       max_seq=256)
+    m, blob, kv = build(qa, tmp_path, h, 21 + n_heads, P)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        t = 5
+        for pos in (P, P + 1):
+            tok_ref, lg_ref = ref.step(t, pos)
+            lg = m.forward([t], pos)
+            assert rel_err(lg, lg_ref) <= 1e-4, pos
+            assert int(np.argmax(lg)) == tok_ref
+            t = tok_ref
+    finally:
+        m.close()
+
+
 def test_decode_short_context_and_tails(qa, tmp_path):
     """Positions 0..9: softmax over N < 8 and N % 8 != 0 keys (the reference's
     libm tail), GQA group 2, three layers."""
