@@ -269,6 +269,12 @@ def test_gemv_softmax_argmax(qa, M, N):
         assert got == int(idx2.download(np.uint32, (1,))[0]) == orc.argmax(logits)
         if tie:
             assert got == min(100, r)
+    # a NaN input makes every logit NaN: index 0 (nothing compares greater)
+    dn = qa.DeviceBuffer.from_numpy(np.full(N, np.nan, np.float32))
+    qa.check(lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dn.ptr, lg.ptr, pr.ptr, idx.ptr, ws.ptr, None))
+    qa.check(lib.qh_device_synchronize())
+    assert np.all(np.isnan(lg.download(np.float32, (M,))))
+    assert int(idx.download(np.uint32, (1,))[0]) == 0
     assert lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dx.ptr, lg.ptr, lg.ptr, idx.ptr, ws.ptr, None) == \
         L.Q_ERR_ALIASING
     assert lib.qh_gemv_q4_f32_softmax_argmax(W.addr, dx.ptr, lg.ptr, pr.ptr, idx.ptr, None, None) == \
