@@ -249,8 +249,14 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     const uint32_t row_bytes = a.nblk * 20u;
     const uint32_t total = a.tile_end[a.nseg - 1];
     const uint32_t stride = gridDim.x * G;
-    const uint32_t pos = a.pos ? __builtin_amdgcn_readfirstlane(*a.pos) : 0u;
-    float rs_norm = a.in_part ? gemv_norm_scale(a.in_part, a.nblk, a.eps) : 1.0f;
+    // The decode position is read with a vector load issued before the x
+    // and weight loads, and turned scalar only where it is used (the RoPE
+    // table rows, the KV-cache address): as a scalar load it would join the
+    // kernel-argument loads, whose lgkmcnt(0) wait would hold every load of
+    // the prologue back by one memory round trip.
+    const __amdgpu_buffer_rsrc_t rpos = __builtin_amdgcn_make_buffer_rsrc((void*)a.pos, 0, a.pos ? 4 : 0, kBufFlags);
+    const uint32_t pos_v = __builtin_amdgcn_raw_buffer_load_b32(rpos, 0, 0, 0);
+    float rs_norm = 1.0f;  // RMSNorm factor: from in_part (after the first tile's loads) or convert_x
 
     uint32_t coff[J];
     bool ok[J];
@@ -472,6 +478,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         const uint32_t hd = a.hd[sg];
         const bool rope = (a.rope_mask >> sg) & 1u;
         const uint32_t hdr = rope ? hd : 0u;
+        const uint32_t pos = __builtin_amdgcn_readfirstlane(pos_v);
         const uint32_t i = rope ? erow % hd : 0u;
         const __amdgpu_buffer_rsrc_t rc =
             __builtin_amdgcn_make_buffer_rsrc((void*)(a.cos_tab + (size_t)pos * hdr), 0, (int)(hdr * 4u), kBufFlags);
@@ -509,6 +516,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         uint32_t sg, tbase;
         seg_of(a, u, sg, tbase);
         const uint32_t row0 = (u - tbase) * RT;
+        const uint32_t pos = __builtin_amdgcn_readfirstlane(pos_v);
         if constexpr (W == 1) {
             if (lane < RT) {
                 float v = acc[0], pv = acc[1];
@@ -554,6 +562,9 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     if constexpr (XF) {
         __builtin_amdgcn_sched_barrier(0);
         convert_x();
+    } else if (a.in_part) {
+        __builtin_amdgcn_sched_barrier(0);
+        rs_norm = gemv_norm_scale(a.in_part, a.nblk, a.eps);
     }
     // The scheduling barriers keep the next tile's loads issued before any
     // instruction that waits on the current tile's data.  (Two tiles of
