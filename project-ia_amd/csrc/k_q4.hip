@@ -842,7 +842,7 @@ static int num_cu() {
 }
 
 // Persistent grid: as many groups of G tiles as are resident at once.
-constexpr int kSwMaxWgPerCu = 3;
+constexpr int kOneWaveMaxWgPerCu = 2;
 
 template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
 static uint32_t gemv_p_grid(uint32_t tiles) {
@@ -855,10 +855,13 @@ static uint32_t gemv_p_grid(uint32_t tiles) {
             o = 1;
         occ = o;
     }
-    // SwiGLU pair mode fits 4 workgroups per CU, but runs faster with 3
-    // (measured: fewer concurrent row streams, decode 521 -> 532 tok/s),
-    // like the other 2-row launches whose registers allow 3.
-    const int per_cu = (SW && occ > kSwMaxWgPerCu) ? kSwMaxWgPerCu : occ;
+    // One-wave launches run at most kOneWaveMaxWgPerCu workgroups per CU
+    // although their registers allow 3 or 4: fewer concurrent row streams
+    // are faster (measured: Q|K|V 7.0 -> 6.25 us, the pair-mode W_gate|W_up
+    // 4 -> 3 per CU took the decode 521 -> 532 tok/s, and 2 per CU gives
+    // 533 -> 544; 1 per CU is slower).  The LM head with argmax partials
+    // keeps its full occupancy (2 per CU was 0.5 us slower there).
+    const int per_cu = (W == 1 && !AM && occ > kOneWaveMaxWgPerCu) ? kOneWaveMaxWgPerCu : occ;
     const uint32_t groups = (tiles + G - 1) / G;
     const uint32_t resident = (uint32_t)(per_cu * num_cu());
     return groups < resident ? groups : resident;
