@@ -841,7 +841,8 @@ static int num_cu() {
     return g_num_cu;
 }
 
-// Persistent grid: as many groups of G tiles as are resident at once.
+// Persistent grid: as many groups of G tiles as are resident at once, with
+// the one-wave shapes limited to kOneWaveMaxWgPerCu workgroups per CU.
 constexpr int kOneWaveMaxWgPerCu = 2;
 
 template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
