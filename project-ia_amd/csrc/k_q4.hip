@@ -842,8 +842,9 @@ static int num_cu() {
 }
 
 // Persistent grid: as many groups of G tiles as are resident at once, with
-// the one-wave shapes limited to kOneWaveMaxWgPerCu workgroups per CU.
-constexpr int kOneWaveMaxWgPerCu = 2;
+// the one-wave shapes limited to 2 or 3 workgroups per CU.
+constexpr int kOneWaveShortWgPerCu = 2;
+constexpr int kOneWaveLongWgPerCu = 3;
 
 template <int W, int J, int G, int RT, bool XF, bool SW = false, bool AM = false>
 static uint32_t gemv_p_grid(uint32_t tiles) {
@@ -856,13 +857,16 @@ static uint32_t gemv_p_grid(uint32_t tiles) {
             o = 1;
         occ = o;
     }
-    // One-wave launches run at most kOneWaveMaxWgPerCu workgroups per CU
-    // although their registers allow 3 or 4: fewer concurrent row streams
-    // are faster (measured: Q|K|V 7.0 -> 6.25 us, the pair-mode W_gate|W_up
-    // 4 -> 3 per CU took the decode 521 -> 532 tok/s, and 2 per CU gives
-    // 533 -> 544; 1 per CU is slower).  The LM head with argmax partials
-    // keeps its full occupancy (2 per CU was 0.5 us slower there).
-    const int per_cu = (W == 1 && !AM && occ > kOneWaveMaxWgPerCu) ? kOneWaveMaxWgPerCu : occ;
+    // One-wave launches run fewer workgroups per CU than their registers
+    // allow (3 or 4): fewer concurrent row streams are faster.  Measured:
+    // launches of at most two tiles per wave at full occupancy (Q|K|V, Wo)
+    // and the pair-mode W_gate|W_up at 2 per CU (Q|K|V 7.0 -> 6.2 us; decode
+    // 521 -> 544 tok/s; 1 per CU is slower); longer launches at 3 (the
+    // 2-segment W_gate|W_up 16.5 us at 2 per CU, 15.65 us at 3).  The LM
+    // head with argmax partials keeps its full occupancy.
+    const uint32_t full_waves = (uint32_t)(occ * num_cu() * G);
+    const int cap = (SW || tiles <= 2u * full_waves) ? kOneWaveShortWgPerCu : kOneWaveLongWgPerCu;
+    const int per_cu = (W == 1 && !AM && occ > cap) ? cap : occ;
     const uint32_t groups = (tiles + G - 1) / G;
     const uint32_t resident = (uint32_t)(per_cu * num_cu());
     return groups < resident ? groups : resident;
