@@ -19,6 +19,9 @@
 //      replaces a top-k set, as in the reference);
 //   5. the token: running fp32 sum over the valid tokens in index order,
 //      the first with r < sum; past the end, the last valid token.
+// Step 1 is applied by the softmax kernels as they read the logits, and
+// step 2's final multiply by 1/sum by k_filter_draw as it reads the
+// exponentials (the same operations, so the same bits).
 // Steps 3-5 run in one workgroup (k_filter_draw) on the nonzero
 // probabilities only: the reference's clamped polynomial exp makes all but a
 // few exactly zero, and a zero is never selected before a nonzero value,
@@ -40,10 +43,22 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__global__ __launch_bounds__(kThreads) void k_scale_temp(const float* __restrict__ x, uint32_t V, uint32_t n_mul,
-                                                       float inv, float t, float* __restrict__ y) {
+// Temperature: x_i * (1/T) over the 8-wide part when the logits are 32-byte
+// aligned (i < n_mul), x_i / T elsewhere (reference main.c:311-427).  The
+// softmax kernels apply it to the logits as they read them.
+struct Temp {
+    uint32_t n_mul;
+    float inv, t;
+};
+
+__device__ __forceinline__ float temp_of(const Temp& tp, const float* __restrict__ x, uint32_t i) {
+    return i < tp.n_mul ? x[i] * tp.inv : x[i] / tp.t;
+}
+
+__global__ __launch_bounds__(kThreads) void k_scale_temp(const float* __restrict__ x, uint32_t V, Temp tp,
+                                                       float* __restrict__ y) {
     const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < V) y[i] = i < n_mul ? x[i] * inv : x[i] / t;
+    if (i < V) y[i] = temp_of(tp, x, i);
 }
 
 // Scalar softmax of compute_softmax_with_temp's fallback (V < 8), one thread.
@@ -76,11 +91,12 @@ __global__ void k_softmax_small(const float* __restrict__ x, uint32_t V, float* 
 // token depends on the exact running sums.)
 constexpr uint32_t kMaxSlice = 4096;
 
-__global__ __launch_bounds__(kThreads) void k_max_part(const float* __restrict__ x, uint32_t V, float* __restrict__ part) {
+__global__ __launch_bounds__(kThreads) void k_max_part(const float* __restrict__ x, uint32_t V, Temp tp,
+                                                     float* __restrict__ part) {
     __shared__ float red[kThreads / 64];
     const uint32_t b0 = blockIdx.x * kMaxSlice, b1 = b0 + kMaxSlice < V ? b0 + kMaxSlice : V;
     float m = -INFINITY;
-    for (uint32_t i = b0 + threadIdx.x; i < b1; i += kThreads) m = fmaxf(m, x[i]);
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += kThreads) m = fmaxf(m, temp_of(tp, x, i));
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
@@ -90,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void k_max_part(const float* __restrict__
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_exp_elems(const float* __restrict__ x, uint32_t V,
+__global__ __launch_bounds__(kThreads) void k_exp_elems(const float* __restrict__ x, uint32_t V, Temp tp,
                                                       const float* __restrict__ part, uint32_t G,
                                                       float* __restrict__ e) {
     float m = -INFINITY;
@@ -98,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void k_exp_elems(const float* __restrict_
     const uint32_t nv = V & ~7u;
     const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
     if (i < V) {
-        const float d = x[i] - m;
+        const float d = temp_of(tp, x, i) - m;
         e[i] = i < nv ? exp_approx(d) : expf(d);
     }
 }
@@ -177,11 +193,6 @@ __global__ __launch_bounds__(64) void k_lane_sums(const float* __restrict__ e, u
     if (lane == 0) out[0] = 1.0f / sum;
 }
 
-__global__ __launch_bounds__(kThreads) void k_scale_by(float* __restrict__ p, uint32_t V, const float* __restrict__ inv) {
-    const float s = *inv;
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < V) p[i] = p[i] * s;
-}
 
 // Valid tokens with nonzero p, in index order (list), their count and the
 // last valid index (a null mask: every token valid): three parallel passes
@@ -312,7 +323,8 @@ constexpr uint32_t kSelThreads = 1024;
 constexpr uint32_t kSelLds = 4096;
 
 struct FilterArgs {
-    const float* p;
+    const float* p;          // probabilities, or the exponentials when inv is set
+    const float* inv;        // null, or 1/sum: p_i = e_i * *inv (the reference's scaling, applied on read)
     uint32_t V;
     const uint32_t* cand;    // nonzero-exponential indices in index order, or null: 0..V-1
     const uint32_t* cand_n;  // their count
@@ -422,6 +434,7 @@ __global__ __launch_bounds__(kSelThreads) void k_filter_draw(FilterArgs a) {
         if (j < nc) {
             i = a.cand ? a.cand[j] : j;
             v = a.p[i];
+            if (a.inv) v = v * *a.inv;
             take = (__float_as_uint(v) & 0x7FFFFFFFu) != 0u;
         }
         const uint64_t bal = __ballot(take);
@@ -622,23 +635,24 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
 
     // 1-2: temperature and softmax; the nonzero exponentials are listed in
     // index order for the sums and the selection
-    QH_K(k_scale_temp, grid, dim3(kThreads), 0, s, logits, V, sp.n_mul, sp.inv_temperature, sp.temperature, scaled);
+    const Temp tp{sp.n_mul, sp.inv_temperature, sp.temperature};
     FilterArgs fa{};
     if (V < 8) {
+        QH_K(k_scale_temp, grid, dim3(kThreads), 0, s, logits, V, tp, scaled);
         QH_K(k_softmax_small, dim3(1), dim3(64), 0, s, scaled, V, probs);
         fa.cand = nullptr;
         fa.cand_n = nullptr;
     } else {
         const uint32_t G = (V + kMaxSlice - 1) / kMaxSlice;
-        QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, scaled, V, smx);
-        QH_K(k_exp_elems, grid, dim3(kThreads), 0, s, scaled, V, smx, G, probs);
+        QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, logits, V, tp, smx);
+        QH_K(k_exp_elems, grid, dim3(kThreads), 0, s, logits, V, tp, smx, G, probs);
         const uint32_t nch = (V + kChunk - 1) / kChunk;
         uint32_t* nzc = reinterpret_cast<uint32_t*>(scal + 8);
         QH_K(k_count, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, nch);
         QH_K(k_scan_chunks, dim3(1), dim3(kThreads), 0, s, chunks, nch, nzc);
         QH_K(k_scatter, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, list);
         QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, probs, V, (const uint32_t*)list, (const uint32_t*)nzc, scal + 6);
-        QH_K(k_scale_by, grid, dim3(kThreads), 0, s, probs, V, scal + 6);
+        fa.inv = scal + 6;  // the filter scales the exponentials as it reads them
         fa.cand = list;
         fa.cand_n = nzc;
     }
