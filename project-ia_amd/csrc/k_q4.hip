@@ -333,13 +333,17 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) xv[i >> 1][4 * (i & 1) + e] = norm ? x4[e] * __uint_as_float(wl[i][e]) : x4[e];
             }
-            // The norm factor scales the row results, not the digits (those
-            // are of x*w): the waves' partial sums share the barrier that
-            // publishes the planes.
             if (norm) {
 #pragma unroll
                 for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
                 if (lane == 0) lds_ss[wave] = ss;
+                __syncthreads();
+                float tot = lds_ss[0];
+#pragma unroll
+                for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
+                const float av = tot / (float)(a.nblk * 32u) + a.eps;
+                const float r0 = __builtin_amdgcn_rsqf(av);
+                rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
             }
             uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
 #pragma unroll
@@ -355,14 +359,6 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
                 }
             }
             __syncthreads();
-            if (norm) {
-                float tot = lds_ss[0];
-#pragma unroll
-                for (int i = 1; i < W * G; ++i) tot += lds_ss[i];
-                const float av = tot / (float)(a.nblk * 32u) + a.eps;
-                const float r0 = __builtin_amdgcn_rsqf(av);
-                rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
-            }
 #pragma unroll
             for (int j = 0; j < J; ++j) {
 #pragma unroll
