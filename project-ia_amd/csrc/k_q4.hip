@@ -925,7 +925,7 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, uint32_t nblk, const uint4
                        const GemvDecode* dec) {
     if (nseg < 1 || nseg > 4) return hipErrorInvalidValue;
     if (nblk <= 64) return run_gemv_p<1, 1, 4, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
-    if (nblk <= 128) return run_gemv_p<1, 2, 4, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
+    if (nblk <= 128) return run_gemv_p<1, 2, 4, 2>(segs, nseg, nblk, xd, nullptr, s, dec);
     if (nblk <= 256) return run_gemv_p<2, 2, 1, 4>(segs, nseg, nblk, xd, nullptr, s, dec);
     if (nblk <= 448) return run_gemv_p<7, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
     if (nblk <= 512) return run_gemv_p<8, 1, 1, 8>(segs, nseg, nblk, xd, nullptr, s, dec);
