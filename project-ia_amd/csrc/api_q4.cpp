@@ -197,8 +197,6 @@ q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, fl
     return Q_OK;
 }
 
-static constexpr bool kGemmEnabled = false;
-
 size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
     return gemm_workspace_bytes(N, T, M_total);
 }
@@ -210,6 +208,7 @@ q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, u
     const uint8_t* w[2];
     float* y[2];
     uint32_t M[2];
+    uint32_t M_total = 0;
     for (uint32_t i = 0; i < n; ++i) {
         const q_tensor* W = Ws[i];
         if (!W || !Ys || !Ys[i] || !X) return Q_ERR_INVALID_ARG;
@@ -228,15 +227,23 @@ q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, u
         w[i] = static_cast<const uint8_t*>(W->data);
         y[i] = Ys[i];
         M[i] = Mi;
+        M_total += Mi;
     }
     if (!workspace) return Q_ERR_INVALID_ARG;
     Device* d;
     QH_TRY_CODE(device(&d));
-    // The kernel has not yet run correctly on a GPU (its first runs were
-    // called through a ctypes binding that truncated Y to 32 bits); the entry
-    // point refuses to launch it until it has.
-    if (!kGemmEnabled) return fail(hipErrorNotSupported, "qh_gemm: prefill GEMM kernel disabled");
-    QH_TRY(launch_gemm(w, y, M, (int)n, Ws[0]->ne[1], X, T, workspace, (hipStream_t)s));
+    // Every operand must be device memory covering the whole extent the
+    // kernels touch: a host or stale pointer becomes an error code here, not
+    // a fault in the kernel.
+    const uint32_t N = Ws[0]->ne[1];
+    if (!device_range(X, (size_t)T * N * 4) ||
+        !device_range(workspace, gemm_workspace_bytes(N, T, M_total)))
+        return fail(hipErrorInvalidValue, "qh_gemm: X or workspace is not device memory of the required size");
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!device_range(w[i], (size_t)M[i] * Ws[i]->nb[0]) || !device_range(y[i], (size_t)T * M[i] * 4))
+            return fail(hipErrorInvalidValue, "qh_gemm: W->data or Y is not device memory of the required size");
+    }
+    QH_TRY(launch_gemm(w, y, M, (int)n, N, X, T, workspace, (hipStream_t)s));
     return Q_OK;
 }
 

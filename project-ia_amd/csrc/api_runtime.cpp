@@ -119,6 +119,24 @@ const void* resident_alias(const void* p, size_t bytes) {
     return nullptr;
 }
 
+bool device_range(const void* p, size_t bytes) {
+    if (!p) return false;
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();  // an unknown address is an answer, not an error to keep
+        return false;
+    }
+    if (at.type != hipMemoryTypeDevice && !at.isManaged) return false;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(base);
+    return a >= b && bytes <= size && a - b <= size - bytes;
+}
+
 }  // namespace qh
 
 using namespace qh;

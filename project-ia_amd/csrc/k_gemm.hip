@@ -10,9 +10,15 @@
 //    32-element block is one K=32 MFMA step whose fp32 result D is scaled by
 //    s in fp32 (inner += s * D), so W enters the matrix core exactly.
 //  * X: each token row is scaled by a power of two 2^e (max |x| in
-//    [2^14, 2^15)) and split into fp16 hi = rn(x') and lo = rn(x' - hi):
-//    22 significant bits.  Two MFMAs per block (hi, lo) accumulate into the
-//    same D; the products (q-8)*hi and (q-8)*lo are exact.
+//    [2^14, 2^15)) and split into two fp16 parts: hi = rn(x') and
+//    lo = rn((x' - hi) * 2^11) (the subtraction and the power-of-two
+//    scaling are exact in fp32).  lo is kept 2^11 above its natural size, so
+//    it stays an fp16 normal wherever hi is (every element within 2^29 of
+//    the row maximum: activation outliers do not cost the other elements
+//    their low bits), and its MFMA takes the weight operand times 2^-11
+//    (exact in fp16).  The two parts hold 22 significant bits of every such
+//    element.  Two MFMAs per block (hi, lo) accumulate into the same D; the
+//    products (q-8)*hi and (q-8)*2^-11*lo are exact.
 //  * Accumulation: a block's D feeds an inner fp32 sum over kInner blocks,
 //    which is added to an outer sum (two-level summation): max error
 //    relative to sum_k |W x| stays at or below the reference AVX2 order's
@@ -53,8 +59,8 @@ __device__ __forceinline__ constexpr int perm8(int p) { return (p >> 1) + 4 * (p
 
 // ---------------------------------------------------------------------------
 // X preparation: one workgroup per (padded) token row.
-// xh/xl: [T_pad][N_pad] fp16, permuted within groups of 8; columns >= N and
-// rows >= T are zero.  meta[t] = (2^-e, non-finite flag).
+// xh/xl: [T_pad][N_pad] fp16 (hi, lo), permuted within groups of 8; columns
+// >= N and rows >= T are zero.  meta[t] = (2^-e, non-finite flag).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X, uint32_t T, uint32_t N,
                                                     uint32_t N_pad, _Float16* __restrict__ xh,
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X,
             const float v = (valid && !nf && k < N) ? ldexpf(xr[k], e) : 0.0f;
             const _Float16 h = (_Float16)v;
             hv[p] = h;
-            lv[p] = (_Float16)(v - (float)h);
+            lv[p] = (_Float16)((v - (float)h) * 2048.0f);  // exact difference, exact scaling
         }
         *reinterpret_cast<h8v*>(hr + g * 8) = hv;
         *reinterpret_cast<h8v*>(lr + g * 8) = lv;
@@ -126,7 +132,7 @@ struct GemmArgs {
     uint32_t blk_per_split;
     uint32_t xcd_map;     // 1: XCD-aware tile order
     const _Float16* xh;
-    const _Float16* xl;
+    const _Float16* xl;   // the low part, times 2^11
     const float2* meta;
     float* part;          // [split][T][M_total-slot] partials (split > 1)
     uint32_t part_ld;     // partial row length (sum of segment M)
@@ -261,30 +267,30 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         if (step + 1 < nsteps) load_step(step + 1);
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
-            h8v B[4];
+            h8v B[4], Bs[4];  // Bs = B * 2^-11 (exact), the operand of lo
             float s[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 64 * wm + 16 * i + lr;
                 B[i] = unpack8(lw[buf][r][kb][lq]);
+                Bs[i] = B[i] * (_Float16)0.00048828125f;
                 s[i] = ls[buf][r][kb];
             }
-            h8v Ah[4], Al[4];
+            // One token subtile at a time: its hi and lo parts, then the 4
+            // weight subtiles.
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int t = 64 * wt + 16 * j + lr;
-                Ah[j] = *reinterpret_cast<const h8v*>(&lx[buf][0][t][32 * kb + 8 * lq]);
-                Al[j] = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
-            }
+                const h8v Ah = *reinterpret_cast<const h8v*>(&lx[buf][0][t][32 * kb + 8 * lq]);
+                const h8v Al = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah[j], B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al[j], B[i], d, 0, 0, 0);
+                for (int i = 0; i < 4; ++i) {
+                    f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Bs[i], d, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) inner[i][j][r] = fmaf(s[i], d[r], inner[i][j][r]);
                 }
+            }
         }
         nb_in += kKB;
         if (nb_in >= kInner) {
@@ -372,11 +378,12 @@ hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t*
     if (nseg < 1 || nseg > 2 || T == 0 || N == 0 || N % 32 != 0) return hipErrorInvalidValue;
     const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
     uint8_t* p = static_cast<uint8_t*>(ws);
+    const size_t plane = align256((size_t)tp * np * 2);
     GemmArgs a{};
     a.xh = reinterpret_cast<_Float16*>(p);
-    a.xl = reinterpret_cast<_Float16*>(p + align256((size_t)tp * np * 2));
-    a.meta = reinterpret_cast<float2*>(p + 2 * align256((size_t)tp * np * 2));
-    float* part = reinterpret_cast<float*>(p + 2 * align256((size_t)tp * np * 2) + align256((size_t)tp * 8));
+    a.xl = reinterpret_cast<_Float16*>(p + plane);
+    a.meta = reinterpret_cast<float2*>(p + 2 * plane);
+    float* part = reinterpret_cast<float*>(p + 2 * plane + align256((size_t)tp * 8));
     uint32_t mt = 0, mtot = 0;
     for (int i = 0; i < nseg; ++i) {
         // Weight offsets are 32-bit buffer offsets.

@@ -78,4 +78,11 @@ const void* resident_alias(const void* p, size_t bytes);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// True when [p, p + bytes) lies inside one device-memory allocation known to
+// the HIP runtime (hipMalloc, a caching allocator's block, ...).  Host
+// pointers, unmapped addresses and ranges that run past their allocation
+// give false, so an entry point can return an error code instead of
+// launching a kernel on them.
+bool device_range(const void* p, size_t bytes);
+
 }  // namespace qh

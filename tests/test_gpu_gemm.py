@@ -7,12 +7,17 @@ restatement (or_gemm_q4_rows) and the fp64 dot product per row.
 
 Tolerance, written out: for every token t and output row m,
     |Y[t,m] - Y64[t,m]| / sum_k |W[m,k] X[t,k]|  <=  1e-5,
-and, per token, the maximum of that statistic must not exceed the AVX2
-order's own maximum by more than 10% (MFMA accumulation order differs from
-the reference's eight-lane order; both sit at the fp32 rounding level,
-~1e-8, three orders of magnitude under the bar).
-At the full config-5 shapes (512 tokens) every row is also checked against
-the GPU GEMV of that token (itself pinned above), a size-independent check.
+and, per token at the BASELINE widths (N >= 4096: config 5's 4096 and
+14336, the GEMV tests' rule for the BASELINE shapes), the maximum of that
+statistic must not exceed the AVX2 order's own maximum by more than 10%
+(the MFMA accumulation order differs from the reference's eight-lane
+order; both sit at the fp32 rounding level, ~1e-8, three orders of
+magnitude under the bar).  Below N = 4096 the bound is three times the
+AVX2 order's maximum: with few blocks the error is the rounding inside each
+block's MFMA partial sum and of the scaled sum over blocks, which for
+N = 96 an exact CPU emulation of that structure (exact X, one rounding per
+block partial) already puts at 1.0-1.5x the AVX2 order's, and the matrix
+core's own summation order adds to it (measured up to 2.2x at N = 96).
 """
 import ctypes as C
 
@@ -21,13 +26,7 @@ import pytest
 
 from oracle import oracle as orc
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason="the first case (M=256 N=4096 T=128) faulted the GPU twice, with two unrelated "
-                            "implementations; the cause, found on the CPU afterwards, was a ctypes binding that "
-                            "passed Y through a 32-bit slot (fixed; test_capi checks every binding). The case "
-                            "stays off the GPU until that fix is run once on its own; qh_gemm_* return an error"),
-]
+pytestmark = pytest.mark.gpu
 
 
 class Gemm:
@@ -53,8 +52,10 @@ class Gemm:
         return [d.download(np.float32, (self.T, M)) for d, M in zip(self.dY, self.Ms)]
 
 
-def check_rows(W, M, N, X, Y, tokens, slack=1.10):
+def check_rows(W, M, N, X, Y, tokens, slack=None):
     """fp64 + AVX2-order comparison for the given token rows."""
+    if slack is None:
+        slack = 1.10 if N >= 4096 else 3.0
     worst, worst_avx = 0.0, 0.0
     for t in tokens:
         y64, cond = orc.gemv_f64(W, M, N, X[t])
@@ -175,6 +176,14 @@ def test_gemm_api_errors(qa):
     assert f(t.addr, dX.ptr, 0, dY.ptr, ws.ptr, None) == -15
     assert f(t.addr, dX.ptr, T, dX.ptr, ws.ptr, None) == -11
     assert f(t.addr, dX.ptr, T, dY.ptr, None, None) == -10
+    # Operands that are not device memory of the needed extent are refused
+    # before any launch: a host X, a Y one row short, a short workspace.
+    hostX = np.zeros((T, N), np.float32)
+    assert f(t.addr, hostX.ctypes.data, T, dY.ptr, ws.ptr, None) == -10
+    short = qa.DeviceBuffer(T * M * 4 - 256)
+    assert f(t.addr, dX.ptr, T, short.ptr, ws.ptr, None) == -10
+    ws_short = qa.DeviceBuffer(lib.qh_gemm_workspace_bytes(N, T, M) - 1024)
+    assert f(t.addr, dX.ptr, T, dY.ptr, ws_short.ptr, None) == -10
     bad = qa.q4_tensor(dW.ptr, M, N)
     bad.t.type = qa.Q_F32
     assert f(bad.addr, dX.ptr, T, dY.ptr, ws.ptr, None) == -14
@@ -184,3 +193,21 @@ def test_gemm_api_errors(qa):
     assert lib.qh_gemm_q4_f32_multi(Ws, Ys, 3, dX.ptr, T, ws.ptr, None) == -15
     assert f(t.addr, dX.ptr, T, dY.ptr, ws.ptr, None) == 0
     assert lib.qh_device_synchronize() == 0
+
+
+def test_gemm_activation_outliers(qa):
+    """Outliers of 1e3, 1e4 and 1e5 on one channel or on one column of every
+    block, meeting a zero weight (nibble 8) in every row: each token row
+    must stay within 1e-5 of fp64 and no worse than the AVX2 order."""
+    from adversarial import CASES, apply_outliers, outlier_columns, set_nibble8
+    for N in (4096, 14336):
+        M = 96
+        rng = orc.rng_for(808, N)
+        chan, per_block = outlier_columns(N, rng)
+        W = set_nibble8(orc.gen_q4(M, N, rng), [chan] + list(per_block))
+        base = rng.standard_normal((len(CASES) + 1, N), dtype=np.float32)
+        X = np.stack([base[0]] + [apply_outliers(base[i + 1], k, m, chan, per_block)
+                                  for i, (k, m) in enumerate(CASES)])
+        (Y,) = Gemm(qa, [W], [M], N, X.shape[0])(X)
+        e, ea = check_rows(W, M, N, X, Y, range(X.shape[0]))
+        print(f"outliers N={N}: max err/cond {e:.3e} (avx2 order {ea:.3e})")
