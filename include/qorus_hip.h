@@ -190,6 +190,21 @@ size_t qh_gemv_softmax_workspace_bytes(uint32_t M);
 q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, float* logits, float* probs,
                                            uint32_t* index_out, void* workspace, qh_stream s);
 
+/* qh_gemv_q4_f32_softmax_argmax without a workspace argument and without
+ * any device allocation: its partials live in a 32 KB array in the
+ * library's device memory, one per GPU, held until the process ends.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same results, bits and validation as the workspace form,
+ * plus: N > 16384 (an input wider than the in-kernel digit conversion,
+ * which would need a digit workspace) -> Q_ERR_INVALID_SIZE.  Every M fits
+ * (the partials of at most 1024 slices, about 25 KB).  Nothing in the array
+ * needs to start at zero (every partial is written before it is read within
+ * a call), but calls that overlap on one GPU share the array and race:
+ * serialize them (one stream, or events between streams). */
+q_error_code qh_gemv_q4_f32_softmax_argmax_noalloc(const q_tensor* W, const float* x, float* logits,
+                                                   float* probs, uint32_t* index_out, qh_stream s);
+
 /* ---- Decode on the device ---- */
 
 /* Greedy generation with no host round trip between steps (no reference

@@ -163,20 +163,26 @@ q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const*
 // 256-byte boundary) the GEMV's argmax partials.
 static size_t lmhead_parts_offset(uint32_t M) { return (softmax_workspace_bytes(M) + 255) & ~(size_t)255; }
 
-size_t qh_gemv_softmax_workspace_bytes(uint32_t M) {
+}  // extern "C"
+
+namespace qh {
+
+size_t gemv_softmax_ws_bytes(uint32_t M) {
     return lmhead_parts_offset(M) + (size_t)2 * kGemvAmaxMaxParts * sizeof(float);
 }
 
-q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, float* logits, float* probs,
-                                           uint32_t* index_out, void* workspace, qh_stream s) {
+q_error_code validate_gemv_softmax(const q_tensor* W, const float* x, const float* logits, const float* probs,
+                                   const uint32_t* index_out) {
     QH_TRY_CODE(validate_gemv(W, x, logits));
-    if (!probs || !index_out || !workspace) return Q_ERR_INVALID_ARG;
+    if (!probs || !index_out) return Q_ERR_INVALID_ARG;
     if (!aligned(probs, 32)) return Q_ERR_MISALIGNED;
     if (probs == logits || probs == x) return Q_ERR_ALIASING;
+    return Q_OK;
+}
+
+q_error_code gemv_softmax_argmax_run(const q_tensor* W, const float* x, float* logits, float* probs,
+                                     uint32_t* index_out, void* workspace, bool may_allocate, hipStream_t st) {
     const uint32_t M = W->ne[0], N = W->ne[1];
-    Device* d;
-    QH_TRY_CODE(device(&d));
-    const hipStream_t st = (hipStream_t)s;
     float* ws = static_cast<float*>(workspace);
     float* parts = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + lmhead_parts_offset(M));
     const GemvSeg seg{static_cast<const uint8_t*>(W->data), logits, nullptr, M};
@@ -191,10 +197,28 @@ q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, fl
     }
     if (e != hipErrorNotSupported) QH_TRY(e);
     void* gws = nullptr;
-    if (needs_workspace(N)) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(N), &gws));
+    if (needs_workspace(N)) {
+        if (!may_allocate) return fail(hipErrorInvalidValue, "input wider than the in-kernel digit conversion");
+        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(N), &gws));
+    }
     QH_TRY(launch_gemv_f32(&seg, 1, N, x, static_cast<uint4*>(gws), st));
     QH_TRY(launch_softmax_argmax_ws(logits, probs, M, ws, index_out, st));
     return Q_OK;
+}
+
+}  // namespace qh
+
+extern "C" {
+
+size_t qh_gemv_softmax_workspace_bytes(uint32_t M) { return gemv_softmax_ws_bytes(M); }
+
+q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, float* logits, float* probs,
+                                           uint32_t* index_out, void* workspace, qh_stream s) {
+    QH_TRY_CODE(validate_gemv_softmax(W, x, logits, probs, index_out));
+    if (!workspace) return Q_ERR_INVALID_ARG;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    return gemv_softmax_argmax_run(W, x, logits, probs, index_out, workspace, true, (hipStream_t)s);
 }
 
 size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {

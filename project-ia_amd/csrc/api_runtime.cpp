@@ -24,6 +24,11 @@ q_error_code fail(hipError_t e, const char* what) {
     return Q_ERR_INVALID_ARG;
 }
 
+q_error_code fail_code(q_error_code code, const char* what) {
+    g_last_error = what;
+    return code;
+}
+
 q_error_code device(Device** out) {
     std::lock_guard<std::mutex> lk(g_init_mu);
     if (!g_dev) {

@@ -17,6 +17,8 @@ namespace qh {
 
 // Records the HIP error text for qh_last_error() and maps it to a q_error_code.
 q_error_code fail(hipError_t e, const char* what);
+// Records `what` for qh_last_error() and returns code.
+q_error_code fail_code(q_error_code code, const char* what);
 
 #define QH_TRY(expr)                                        \
     do {                                                    \
@@ -77,6 +79,21 @@ void ctx_state_erase(const q_context* ctx);
 const void* resident_alias(const void* p, size_t bytes);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// GEMV argument checks of reference src/ops/avx2/matmul.c:104-197 plus the
+// device-side ones (api_q4.cpp), shared by every GEMV entry point.
+q_error_code validate_gemv(const q_tensor* W, const float* x, const float* y);
+
+// LM head + softmax + greedy argmax (qh_gemv_q4_f32_softmax_argmax): the
+// argument checks, the workspace size for M logits, and the launches on st
+// with that workspace.  Inputs wider than the in-kernel digit conversion
+// need a digit workspace, taken from the library's own allocation only when
+// may_allocate (else the call fails).
+size_t gemv_softmax_ws_bytes(uint32_t M);
+q_error_code validate_gemv_softmax(const q_tensor* W, const float* x, const float* logits, const float* probs,
+                                   const uint32_t* index_out);
+q_error_code gemv_softmax_argmax_run(const q_tensor* W, const float* x, float* logits, float* probs,
+                                     uint32_t* index_out, void* workspace, bool may_allocate, hipStream_t st);
 
 // True when [p, p + bytes) lies inside one device-memory allocation known to
 // the HIP runtime (hipMalloc, a caching allocator's block, ...).  Host

@@ -167,6 +167,7 @@ def lib():
     _sig(L, "qh_softmax_argmax_f32_ws", i32, vp, vp, u32, vp, vp, vp)
     _sig(L, "qh_gemv_softmax_workspace_bytes", C.c_size_t, u32)
     _sig(L, "qh_gemv_q4_f32_softmax_argmax", i32, vp, vp, vp, vp, vp, vp, vp)
+    _sig(L, "qh_gemv_q4_f32_softmax_argmax_noalloc", i32, vp, vp, vp, vp, vp, vp)
     _sig(L, "qh_add_f32", i32, vp, vp, vp, u32, vp)
     _sig(L, "qh_mul_f32", i32, vp, vp, vp, u32, vp)
     _sig(L, "qh_argmax_f32", i32, vp, u32, vp, vp)
