@@ -480,6 +480,54 @@ def ref_matmul(A, B):
     return rc, Cm.copy()
 
 
+class _RefModel(C.Structure):
+    """q_llama_model of reference include/qorus_types.h:265-286 (x86-64)."""
+    _fields_ = [("config", C.c_uint32 * 9), ("token_embd", C.c_void_p), ("output_norm", C.c_void_p),
+                ("output", C.c_void_p), ("layers", C.c_void_p), ("rope_freqs", C.c_void_p),
+                ("rope_cache_enabled", C.c_bool), ("rope_cos_cache", C.c_void_p),
+                ("rope_sin_cache", C.c_void_p), ("ctx", C.c_void_p)]
+
+
+def ref_rope_cache(tmp_dir, head_dim: int, max_seq: int, base: float):
+    """The RoPE cos/sin cache [max_seq][head_dim] that the reference's own
+    llama_build_graph builds (src/models/model.c:625-665), from a file in the
+    reference's layout (model.c:352-618: FP32 output, [in, out] shapes) whose
+    tensors are zero.  Returns (rc, cos, sin)."""
+    R = ref()
+    R.q_init_memory.restype = C.c_int
+    R.q_init_memory.argtypes = [C.c_void_p, C.c_char_p]
+    R.q_alloc_arena.restype = C.c_int
+    R.q_alloc_arena.argtypes = [C.c_void_p, C.c_size_t]
+    R.llama_build_graph.restype = C.c_int
+    R.llama_build_graph.argtypes = [C.c_void_p, C.c_void_p]
+    R.q_free_memory.restype = None
+    R.q_free_memory.argtypes = [C.c_void_p]
+    vocab, n_heads, n_layers = 64, 2, 1
+    dim = head_dim * n_heads
+    hidden, kvd = dim, dim
+    q4 = lambda rows, cols: rows * (cols // 32) * 20
+    size = 64 + _al(vocab * dim * 4) * 2 + _al(dim * 4)
+    size += n_layers * (2 * _al(dim * 4) + 2 * _al(q4(dim, dim)) + 2 * _al(q4(dim, kvd)) + 3 * _al(q4(dim, hidden)))
+    head = struct.pack("<9I2f5I", 0x514F5231, 3, vocab, dim, hidden, n_layers, n_heads, n_heads, max_seq,
+                       base, 1e-5, 0, 0, 0, 0, 0)
+    path = Path(tmp_dir) / "ref_rope_layout.qorus"
+    path.write_bytes(head + bytes(size - 64))
+    ctx = _RefCtx()
+    model = _RefModel()
+    rc = R.q_init_memory(C.addressof(ctx), str(path).encode())
+    cos = sin = None
+    if rc == Q_OK:
+        rc = R.q_alloc_arena(C.addressof(ctx), 2 * max_seq * head_dim * 4 + (1 << 20))
+    if rc == Q_OK:
+        rc = R.llama_build_graph(C.addressof(ctx), C.addressof(model))
+    if rc == Q_OK and model.rope_cache_enabled:
+        n = max_seq * head_dim
+        cos = np.ctypeslib.as_array((C.c_float * n).from_address(model.rope_cos_cache)).reshape(max_seq, head_dim).copy()
+        sin = np.ctypeslib.as_array((C.c_float * n).from_address(model.rope_sin_cache)).reshape(max_seq, head_dim).copy()
+    R.q_free_memory(C.addressof(ctx))
+    return rc, cos, sin
+
+
 # ---------------------------------------------------------------------------
 # .qorus v3 layout (corrected Llama-3 shapes, Q4_0 LM head) -- an independent
 # restatement of the tensor order of reference src/models/model.c:352-618.

@@ -18,9 +18,12 @@
  *                      oracle/_ref (rsqrtps seed is CPU-specific, so bits are
  *                      not portable: parity is tolerance-only by nature).
  *   or_rope            bit-equality with oracle/_ref; rotation invariants.
- *   or_rope_tables     same libm calls and expression order as the
- *                      reference's table builder; parity at the libm
- *                      boundary is unpinned (no reference fixture holds it).
+ *   or_rope_tables     bit-equality, every position 0..2047 and every
+ *                      pair, with the cache the reference's own
+ *                      llama_build_graph builds in oracle/_ref (head_dim
+ *                      128/base 500000 and 64/10000); each entry within 1 ulp
+ *                      of float64 cos/sin along the builder's float32 chain
+ *                      freq_i = base^(-2i/hd), theta = freq_i * pos.
  *   or_exp_approx      bit-equality with oracle/_ref's softmax/silu outputs;
  *                      polynomial special cases (x<-10 -> 0, x>10 -> 22026).
  *   or_silu/softmax    bit-equality with oracle/_ref on the vector part; the
@@ -40,12 +43,17 @@
  *   or_dot_f32/matmul  bit-equality with oracle/_ref's q_matmul_f32_avx2.
  *   or_attention_decode  composition of the above; fp64 textbook attention
  *                      (with the polynomial exp) within tolerance.
- *   or_decode_step     composition; no reference fixture exists because the
- *                      reference forward never reads its KV cache and writes
- *                      FP32 bytes into Q4 slots of its dummy model.  Pinned
- *                      only through its parts: the composition itself is
- *                      "parity unpinned" beyond argmax agreement with an
- *                      fp64 restatement.
+ *   or_decode_step     no reference fixture exists (the reference forward
+ *                      never reads its KV cache and its dummy model holds
+ *                      FP32 bytes in Q4 slots).  Pinned through its parts and,
+ *                      as a composition, against a float64 restatement
+ *                      written from the Llama-3 equations (tests/llama_f64.py):
+ *                      same greedy token, logits within 1e-4 of the largest
+ *                      |logit| and the same cache row, on 2-layer models with
+ *                      GQA groups 1/2/4 at pos 0 and at pos 13 over a random
+ *                      cache; planted composition mistakes (GQA mapping,
+ *                      RoPE position or pairing, residual, norm weight) fail
+ *                      that comparison.
  */
 #include "qorus_oracle.h"
 

@@ -314,3 +314,93 @@ def test_attention_gqa_mapping_and_causality():
     q = np.zeros(n_heads * hd, np.float32)
     out = orc.attention_decode(q, kv, n_heads, n_kv, hd, max_seq, pos).reshape(n_heads, hd)
     assert np.all(out[:4] == 0.0) and np.allclose(out[4:], 1.0)
+
+
+# ----------------------------------------------------------- RoPE tables --
+
+@needs_ref
+@pytest.mark.parametrize("hd,base", [(128, 500000.0), (64, 10000.0)])
+def test_rope_tables_match_reference_build_every_pair(tmp_path, hd, base):
+    """Every position and pair of or_rope_tables against the cache that the
+    reference's own llama_build_graph builds (src/models/model.c:625-665)."""
+    max_seq = 2048
+    rc, cr, sr = orc.ref_rope_cache(tmp_path, hd, max_seq, base)
+    assert rc == 0 and cr is not None
+    for pos in range(max_seq):
+        c, s = orc.rope_tables(base, hd, pos)
+        assert np.array_equal(bits(c), bits(cr[pos])) and np.array_equal(bits(s), bits(sr[pos])), pos
+
+
+def test_rope_tables_closed_form_every_pair():
+    """freq_i = base^(-2i/head_dim), theta = freq_i * pos, cos/sin duplicated
+    per pair: each entry within 1 ulp of the float64 cos/sin of theta, where
+    the exponent -2i/hd, freq (within 1 ulp of the float64 power) and theta
+    follow the float32 expression chain of the table builder."""
+    base, hd = np.float32(500000.0), 128
+    for pos in (1, 2, 777, 2047):
+        c, s = orc.rope_tables(float(base), hd, pos)
+        assert np.array_equal(c[0::2], c[1::2]) and np.array_equal(s[0::2], s[1::2])
+        for i in range(hd // 2):
+            fe = np.float32(np.float32(-2.0) * np.float32(i)) / np.float32(hd)
+            f32 = np.float32(float(base) ** float(fe))
+            ok = False
+            for f in (np.nextafter(f32, np.float32(-np.inf)), f32, np.nextafter(f32, np.float32(np.inf))):
+                th = float(np.float32(f * np.float32(pos)))
+                cu = float(np.spacing(np.float32(abs(c[2 * i]))))
+                su = float(np.spacing(np.float32(abs(s[2 * i]))))
+                if abs(float(c[2 * i]) - math.cos(th)) <= cu and abs(float(s[2 * i]) - math.sin(th)) <= su:
+                    ok = True
+            assert ok, (pos, i)
+
+
+# ------------------------------------------------------------ decode step --
+
+def _tiny_model(tmp_path, n_kv, seed):
+    from qorus_amd.model_file import QorusHeader
+    from qorus_amd.synthetic import write_synthetic_model
+    h = QorusHeader(vocab=512, dim=256, hidden=320, n_layers=2, n_heads=4, n_kv=n_kv, max_seq=32)
+    path = tmp_path / f"tiny_{n_kv}_{seed}.qorus"
+    write_synthetic_model(path, h, seed)
+    return h, np.fromfile(path, dtype=np.uint8)
+
+
+def _kv_for(h, pos, seed):
+    kv = np.zeros((h.n_layers, h.n_kv, h.max_seq, 2, h.head_dim), np.float32)
+    kv[:, :, :pos] = orc.rng_for(seed, pos).standard_normal(kv[:, :, :pos].shape, dtype=np.float32)
+    return kv
+
+
+def _step_both(tmp_path, n_kv, pos, seed=71, token=37):
+    from llama_f64 import Llama64
+    h, blob = _tiny_model(tmp_path, n_kv, seed)
+    kv = _kv_for(h, pos, seed)
+    ref64 = Llama64(blob, kv)
+    tok, logits = orc.DecodeOracle(blob, kv).step(token, pos)  # kv updated in place
+    return h, ref64, kv, tok, logits
+
+
+@pytest.mark.parametrize("n_kv", [4, 2, 1])  # GQA groups 1, 2, 4
+@pytest.mark.parametrize("pos", [0, 13])     # empty cache; 14 keys (a softmax tail of 6)
+def test_decode_step_vs_fp64(tmp_path, n_kv, pos):
+    """or_decode_step against the float64 restatement written from the
+    Llama-3 equations (tests/llama_f64.py): same greedy token, logits within
+    1e-4 of the largest |logit|, and the cache row written at pos."""
+    h, ref64, kv, tok, logits = _step_both(tmp_path, n_kv, pos)
+    tok64, logits64 = ref64.step(37, pos)
+    scale = float(np.max(np.abs(logits64)))
+    assert tok == tok64
+    assert float(np.max(np.abs(logits.astype(np.float64) - logits64))) <= 1e-4 * scale
+    kv_err = np.max(np.abs(kv[:, :, pos].astype(np.float64) - ref64.kv[:, :, pos]))
+    assert kv_err <= 1e-4 * float(np.max(np.abs(ref64.kv[:, :, pos])))
+
+
+@pytest.mark.parametrize("mistake", ["gqa", "rope_pos", "rope_pairs", "residual", "norm_weight"])
+def test_decode_fp64_comparison_catches_planted_mistakes(tmp_path, mistake):
+    """The comparison above has teeth: one wrong composition step planted in
+    the float64 restatement (GQA head mapping h % n_kv, RoPE at pos + 1,
+    rotate-half pairs, the MLP residual taken from x instead of x1, the FFN
+    norm weight in the attention norm) breaks it."""
+    _, ref64, _, tok, logits = _step_both(tmp_path, 2, 13)
+    tok64, logits64 = ref64.step(37, 13, mistake=mistake)
+    scale = float(np.max(np.abs(logits64)))
+    assert tok != tok64 or float(np.max(np.abs(logits.astype(np.float64) - logits64))) > 1e-4 * scale
