@@ -21,12 +21,22 @@
 //    load covers 1280 contiguous bytes of a row.
 //  * Partial sums are reduced across the wave by butterflies and across
 //    waves through LDS in a fixed order (deterministic).
-// Accuracy (fp64-referenced, relative to sum_j |W_ij x_j|): ~1e-8, below
-// the reference AVX2 order's own error at Llama-3 shapes.
+// Outliers: a block whose largest element carries more than 3/4 of the
+// block's magnitude (an activation outlier) also gets a second level of
+// digits for the residual x*2^k - x_int, so every element within 2^22 of
+// the block maximum is represented exactly (qh_digits.hpp); the GEMV adds
+// that level's dot, one plane at a time, only in waves whose columns hold
+// such a block (found at the barrier that publishes the digits, or with
+// the digits themselves), in a loop of its own without prefetch so the
+// level-1 loop keeps its registers and occupancy.
+// Accuracy (fp64-referenced, relative to sum_j |W_ij x_j|): 0.4-2e-8 at the
+// Llama-3 shapes with N(0,1) inputs, at or below the reference AVX2 order's,
+// and the same with outliers of 1e3..1e5 meeting zero weights (tested).
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
 #include <cstdint>
+#include <type_traits>
 
 #include "qh_kernels.hpp"
 #include "qh_digits.hpp"
@@ -265,7 +275,12 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     uint32_t am_i = 0xFFFFFFFFu;
     int kk[J];
     float zz[J];
+    uint32_t wd[J];  // the columns' wide flags (blocks with level-2 digits)
     uint32_t cols[J];
+    // Does the workgroup (fp32 input by lane quads), the wave (wave-local
+    // conversion) or, tile by tile, the wave (prepared digits) hold a block
+    // that needs level 2?
+    bool use_lo = false;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t col = (uint32_t)((j * W + kw) * 64 + lane);
@@ -289,9 +304,16 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
     constexpr int kQPass = XF ? (4 * kMaxBlk + kThreads - 1) / kThreads : 0;
     constexpr int kLd = XF ? (kWaveLocal ? 8 : 2 * kQPass) : 0;
     constexpr int kXs = 36;
-    constexpr int kLds = !XF ? 1 : (kWaveLocal && kMaxBlk * kXs / 4 > 7 * kMaxBlk ? kMaxBlk * kXs / 4 : 7 * kMaxBlk);
+    // LDS: the quad path keeps all 13 planes of every block (levels 1 and 2:
+    // level 2 is read per tile when the wave holds a wide block); the
+    // wave-local path stages x at kXs floats per block, and each wave then
+    // keeps its blocks' level-2 planes in its own part of that staging area
+    // (6 * 64 uint4 of its 64 * kXs / 4).
+    static_assert(!kWaveLocal || 6 * 64 * 4 <= 64 * kXs, "wave-local level-2 planes must fit the wave's staging");
+    constexpr int kLds = !XF ? 1 : (kWaveLocal ? kMaxBlk * kXs / 4 : kXdPlanes * kMaxBlk);
     __shared__ uint4 lds[kLds];
     __shared__ float lds_ss[XF ? W * G : 1];
+    __shared__ uint32_t lds_wide[XF ? W * G : 1];  // per wave: converted a wide block
     v4u32 xl[kLd > 0 ? kLd : 1], wl[kLd > 0 ? kLd : 1];
     if constexpr (XF) {
         const __amdgpu_buffer_rsrc_t rx =
@@ -307,7 +329,7 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
     } else {
-        load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz);
+        load_digits<J>(a.xd, a.pad, cols, ok, xp, kk, zz, wd);
     }
     // x (or x*w with the RMSNorm weight) staged, converted, and the digits
     // of this lane's columns loaded.  RMSNorm: the sum of x^2 is taken per
@@ -346,26 +368,47 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
                 rs_norm = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
             }
             uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
+            bool wide_here = false;
 #pragma unroll
             for (int ps = 0; ps < kQPass; ++ps) {
                 const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
                 const uint32_t c = t >> 2, qi = t & 3u;
-                uint32_t pl[6], kq, zq;
-                prep_quarter(xv[ps], pl, kq, zq);  // whole quads share c, so they agree on c < kMaxBlk
+                uint32_t pl[6], kq, zq, wq;
+                prep_quarter(xv[ps], pl, kq, zq, wq);  // whole quads share c, so they agree on c < kMaxBlk
                 if (c < (uint32_t)kMaxBlk) {
 #pragma unroll
                     for (int p = 0; p < 6; ++p) ldw[((uint32_t)p * kMaxBlk + c) * 4u + qi] = pl[p];
-                    ldw[(6u * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : 0u);
+                    ldw[(kXdMeta * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : (qi == 2 ? wq : 0u));
+                }
+                // Level 2 of a wide block (the others' stay unwritten: their
+                // readers go by the wide flag).
+                if (wq && c < (uint32_t)kMaxBlk) {
+                    uint32_t pl2[6];
+                    prep_quarter_lo(xv[ps], (int)kq, pl2);
+#pragma unroll
+                    for (int p = 0; p < 6; ++p) ldw[((kXdLo + (uint32_t)p) * kMaxBlk + c) * 4u + qi] = pl2[p];
+                    wide_here = true;
                 }
             }
+            // The barrier that publishes the digits also publishes each
+            // wave's "converted a wide block" word; every wave ORs them (it
+            // reads all or half of the blocks).  The words are read before
+            // the digits, so the decision waits for one LDS read only.
+            const bool wave_wide = __ballot(wide_here) != 0ull;  // whole wave votes
+            if (lane == 0) lds_wide[wave] = wave_wide ? 1u : 0u;
             __syncthreads();
+            uint32_t wide_any = 0u;
+#pragma unroll
+            for (int i = 0; i < W * G; ++i) wide_any |= lds_wide[i];
+            use_lo = wide_any != 0u;
 #pragma unroll
             for (int j = 0; j < J; ++j) {
 #pragma unroll
                 for (int p = 0; p < 6; ++p) xp[j][p] = lds[p * kMaxBlk + cols[j]];
-                const uint4 m = lds[6 * kMaxBlk + cols[j]];
+                const uint4 m = lds[kXdMeta * kMaxBlk + cols[j]];
                 kk[j] = ok[j] ? (int)m.x : 0;
                 zz[j] = ok[j] ? __uint_as_float(m.y) : 0.0f;
+                wd[j] = ok[j] ? m.z : 0u;
             }
         } else {
             // One block per lane, staged through LDS inside the wave.
@@ -412,12 +455,22 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
                 xw[4 * i + 2] = __uint_as_float(v[2]);
                 xw[4 * i + 3] = __uint_as_float(v[3]);
             }
-            uint4 o[7];
+            uint4 o[13];
             prep_block(xw, o);
 #pragma unroll
             for (int p = 0; p < 6; ++p) xp[0][p] = o[p];
-            kk[0] = ok[0] ? (int)o[6].x : 0;
-            zz[0] = ok[0] ? __uint_as_float(o[6].y) : 0.0f;
+            kk[0] = ok[0] ? (int)o[kXdMeta].x : 0;
+            zz[0] = ok[0] ? __uint_as_float(o[kXdMeta].y) : 0.0f;
+            wd[0] = ok[0] ? o[kXdMeta].z : 0u;
+            use_lo = __ballot(wd[0] != 0u) != 0ull;
+            // Level-2 planes into this wave's own staging rows, which this
+            // lane's reads above have already consumed (a wave's LDS
+            // operations complete in order).
+            if (wd[0]) {
+                uint4* lo2 = reinterpret_cast<uint4*>(xs + (uint32_t)(kw * 64) * kXs);
+#pragma unroll
+                for (int p = 0; p < 6; ++p) lo2[p * 64 + lane] = o[kXdLo + p];
+            }
         }
     };
 
@@ -488,11 +541,37 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         e.sn = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rn, i * 4u, 0, 0));
     };
 
-    auto finish_tile = [&](uint32_t u, const uint4 (&q)[RT][J], const float (&s)[RT][J], const Epi& e) {
+    // Level-2 plane p of this lane's column j: from LDS (fp32 input) or from
+    // the prepared digits in HBM.
+    auto lo_plane = [&](int j, int p, uint32_t salt) -> uint4 {
+        if constexpr (XF) {
+            if constexpr (kWaveLocal) {
+                const uint4* w2 = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(lds) +
+                                                                 (uint32_t)(kw * 64) * kXs) + (lane + salt);
+                return w2[p * 64];
+            } else {
+                return (lds + (cols[j] + salt))[(kXdLo + (uint32_t)p) * kMaxBlk];
+            }
+        } else {
+            return load_lo_plane(a.xd, a.pad, cols[j], ok[j], p, salt);
+        }
+    };
+    // Cross-wave partial sums of a tile (W > 1).  Declared here, not in the
+    // lambda below: each instantiation of a generic lambda would get its own
+    // array, and waves of one workgroup may run different instantiations.
+    __shared__ float red[W > 1 ? W : 1][RT];
+
+    // lo2: std::true_type for the level-1 + level-2 dot, std::false_type for
+    // level 1 alone.
+    auto finish_tile = [&](auto lo2, uint32_t u, const uint4 (&q)[RT][J], const float (&s)[RT][J], const Epi& e) {
         float acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = 0.0f;
-        dot_batch<RT, J>(q, s, xp, kk, zz, ok, acc);
+        if constexpr (std::is_same_v<decltype(lo2), std::true_type>) {
+            dot_batch2<RT, J>(q, s, xp, lo_plane, kk, zz, ok, wd, acc);
+        } else {
+            dot_batch<RT, J>(q, s, xp, kk, zz, ok, acc);
+        }
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             float v = acc[r];
@@ -534,7 +613,6 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
                 }
             }
         } else {
-            __shared__ float red[W][RT];
             if (lane == 0) {
 #pragma unroll
                 for (int r = 0; r < RT; ++r) red[kw][r] = acc[r];
@@ -566,21 +644,76 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         rs_norm = gemv_norm_scale(a.in_part, a.nblk, a.eps);
     }
-    // The scheduling barriers keep the next tile's loads issued before any
+    // Level 1 + 2, one tile at a time: no prefetch, so the level-2
+    // registers fit in those of a prefetched tile and the kernel keeps the
+    // occupancy of the level-1 loop.
+    auto level2_loop = [&]() {
+        while (u < total) {
+            finish_tile(std::true_type{}, u, qa, sa, ea);
+            u += stride;
+            if (u >= total) break;
+            load_tile(u, qa, sa, ea);
+        }
+    };
+    // Level 1, double-buffered: qa holds tile u; each half step issues the
+    // next tile's loads, then the scheduling barrier keeps them ahead of any
     // instruction that waits on the current tile's data.  (Two tiles of
-    // prefetch measured slower: more concurrent row streams.)
-    while (u < total) {
-        uint32_t un = u + stride;
-        load_tile(un, qb, sb, eb);
-        __builtin_amdgcn_sched_barrier(0);
-        finish_tile(u, qa, sa, ea);
-        u = un;
-        if (u >= total) break;
-        un = u + stride;
-        load_tile(un, qa, sa, ea);
-        __builtin_amdgcn_sched_barrier(0);
-        finish_tile(u, qb, sb, eb);
-        u = un;
+    // prefetch measured slower: more concurrent row streams; so did a loop
+    // entered with the next tile already issued.)
+    auto level1_loop = [&]() {
+        while (u < total) {
+            uint32_t un = u + stride;
+            load_tile(un, qb, sb, eb);
+            __builtin_amdgcn_sched_barrier(0);
+            finish_tile(std::false_type{}, u, qa, sa, ea);
+            u = un;
+            if (u >= total) break;
+            un = u + stride;
+            load_tile(un, qa, sa, ea);
+            __builtin_amdgcn_sched_barrier(0);
+            finish_tile(std::false_type{}, u, qb, sb, eb);
+            u = un;
+        }
+    };
+    if constexpr (XF) {
+        // The conversion has already set use_lo (no wait on memory).
+        if (use_lo)
+            level2_loop();
+        else
+            level1_loop();
+    } else {
+        // Prepared digits: the wide flags arrive with the digits, so the
+        // second tile's loads go out before waiting on them (a level-2 run
+        // drops that tile and loads it again), and the first step of the
+        // level-1 loop is peeled.  With waves splitting K the choice is made
+        // workgroup-uniform (the cross-wave reduction has barriers in it);
+        // not a decode-step shape.
+        if (u < total) {
+            uint32_t un = u + stride;
+            load_tile(un, qb, sb, eb);
+            __builtin_amdgcn_sched_barrier(0);
+            bool any = false;
+#pragma unroll
+            for (int j = 0; j < J; ++j) any = any || (ok[j] && wd[j] != 0u);
+            if constexpr (W > 1)
+                use_lo = __syncthreads_or(any) != 0;
+            else
+                use_lo = __ballot(any) != 0ull;
+            if (use_lo) {
+                level2_loop();
+            } else {
+                finish_tile(std::false_type{}, u, qa, sa, ea);
+                u = un;
+                if (u < total) {
+                    un = u + stride;
+                    load_tile(un, qa, sa, ea);
+                    __builtin_amdgcn_sched_barrier(0);
+                    finish_tile(std::false_type{}, u, qb, sb, eb);
+                    u = un;
+                    level1_loop();
+                }
+            }
+        }
     }
     if constexpr (AM) {
         // Every wave reaches this point (the loop only breaks).
@@ -679,59 +812,65 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv(const GemvArgs a) {
         uint4 xp[J][6];
         int kk[J];
         float zz[J];
+        uint32_t cols[J];
+        uint32_t wd[J];
+        bool any = false;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t cc = coff[j] / 20u;
+            cols[j] = cc;
 #pragma unroll
             for (int p = 0; p < 6; ++p) {
                 const uint4 v = a.xd[(size_t)p * a.pad + cc];
                 xp[j][p] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
             }
-            const uint4 meta = a.xd[(size_t)6 * a.pad + cc];
+            const uint4 meta = a.xd[(size_t)kXdMeta * a.pad + cc];
             kk[j] = ok[j] ? (int)meta.x : 0;
             zz[j] = ok[j] ? __uint_as_float(meta.y) : 0.0f;
+            wd[j] = ok[j] ? meta.z : 0u;
+            any = any || wd[j] != 0u;
         }
+        const bool wave_wide = __ballot(any) != 0ull;
+        auto lo_plane = [&](int j, int p, uint32_t salt) -> uint4 {
+            return load_lo_plane(a.xd, a.pad, cols[j], ok[j], p, salt);
+        };
 
+        if (wave_wide) {
+            // Level 1 + 2, one batch at a time (no prefetch: the level-2
+            // registers fit in those of the prefetched batch).
+            static_assert(R % 2 == 0, "the level-2 path runs rows in pairs");
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (b + 1 < NB) load_batch(b + 1, (b + 1) & 1);
-            // Integer dots of the R*J blocks of this batch, plane by plane
-            // across all blocks: each plane is a 4-deep dot8 chain of its
-            // own and the planes combine by P = (P << 4) + S_p, so the
-            // independent chains of different blocks interleave.
-            int P[R][J];
-            uint32_t wq[R][J][4];
+            for (int b = 0; b < NB; ++b) {
+                if (b > 0) load_batch(b, 0);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+                for (int h = 0; h < R / 2; ++h) {
+                    uint4 qh[2][J];
+                    float sh[2][J], part[2];
 #pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const uint4 qq = q[b & 1][r][j];
-                    wq[r][j][0] = qq.x ^ 0x88888888u;
-                    wq[r][j][1] = qq.y ^ 0x88888888u;
-                    wq[r][j][2] = qq.z ^ 0x88888888u;
-                    wq[r][j][3] = qq.w ^ 0x88888888u;
-                    P[r][j] = 0;
-                }
+                    for (int r = 0; r < 2; ++r) {
 #pragma unroll
-            for (int p = 5; p >= 0; --p)
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-#pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        int sp = __builtin_amdgcn_sdot8((int)wq[r][j][0], (int)xp[j][p].x, 0, false);
-                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][1], (int)xp[j][p].y, sp, false);
-                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][2], (int)xp[j][p].z, sp, false);
-                        sp = __builtin_amdgcn_sdot8((int)wq[r][j][3], (int)xp[j][p].w, sp, false);
-                        P[r][j] = (int)((uint32_t)P[r][j] << 4) + sp;
+                        for (int j = 0; j < J; ++j) {
+                            qh[r][j] = q[0][2 * h + r][j];
+                            sh[r][j] = s[0][2 * h + r][j];
+                        }
+                        part[r] = acc[b * R + 2 * h + r];
                     }
+                    dot_batch2<2, J>(qh, sh, xp, lo_plane, kk, zz, ok, wd, part);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const float sc = ok[j] ? s[b & 1][r][j] : 0.0f;
-                    const float c = fmaf(sc, (float)P[r][j], zz[j]);
-                    acc[b * R + r] += ldexpf(c, -kk[j]);
+                    for (int r = 0; r < 2; ++r) acc[b * R + 2 * h + r] = part[r];
                 }
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (b + 1 < NB) load_batch(b + 1, (b + 1) & 1);
+                float part[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) part[r] = acc[b * R + r];
+                dot_batch<R, J>(q[b & 1], s[b & 1], xp, kk, zz, ok, part);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[b * R + r] = part[r];
+            }
         }
     }
 

@@ -16,9 +16,11 @@ namespace qh {
 hipError_t launch_dequant(const uint8_t* blocks, float* out, uint64_t n_blocks, hipStream_t s);
 
 // x-digit planes ("xd"): per 32-element block of x, the signed 4-bit digits
-// of round(x * 2^k) in 6 planes (uint4 each), plus (k, NaN-injection word).
-// Layout: uint4 xd[7][nblk_pad]; plane t of block c at xd[t * nblk_pad + c].
-constexpr int kXdPlanes = 7;
+// of round(x * 2^k) in 6 planes (uint4 each), a meta word (k, NaN-injection
+// word, wide flag, 0), and 6 planes of the residual's digits for blocks
+// holding an outlier (qh_digits.hpp).  Layout: uint4 xd[13][nblk_pad];
+// plane t of block c at xd[t * nblk_pad + c].
+constexpr int kXdPlanes = 13;
 inline uint32_t xd_pad(uint32_t nblk) { return (nblk + 63u) & ~63u; }
 inline size_t xd_bytes(uint32_t nblk) { return (size_t)kXdPlanes * xd_pad(nblk) * 16u; }
 
