@@ -129,10 +129,15 @@ q_error_code llama_forward(q_llama_model* Q_RESTRICT model, q_context* Q_RESTRIC
                            const uint32_t* Q_RESTRICT tokens, uint32_t seq_len,
                            uint32_t pos, float* Q_RESTRICT logits);
 
-/* Greedy (temperature < 1e-6) token selection: first index of the maximum.
- * Sampling with temperature/top-k/top-p is not part of this build and
- * returns Q_ERR_INVALID_ARG.
- * Replaces reference qorus.h:292-300 / src/main.c:852-881. */
+/* Next-token selection on the GPU, with the reference's validation order,
+ * arena allocations and thread-local xorshift64* stream.  temperature <
+ * 1e-6: greedy, the first index of the maximum.  Otherwise softmax of
+ * logits / temperature in the reference's order, then top-k and/or top-p
+ * filtering and one draw; equal probabilities at a top-k/top-p cut keep the
+ * lower indices, and with neither filter every token is a candidate (two
+ * cases the reference leaves to its sort internals or unwritten memory).
+ * logits are host memory, as in the reference.
+ * Replaces reference qorus.h:285-300 / src/main.c:852-992. */
 q_error_code q_sample_token(const float* Q_RESTRICT logits, uint32_t vocab_size,
                             float temperature, uint32_t top_k, float top_p,
                             uint32_t* Q_RESTRICT token_id_out, q_context* Q_RESTRICT ctx);
