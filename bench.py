@@ -467,6 +467,129 @@ def run_cpu_lmhead(n_steps=3):
 
 
 # ---------------------------------------------------------------------------
+# Config 5: batched prefill GEMM on MFMA
+# ---------------------------------------------------------------------------
+PREFILL_T = 512
+PREFILL_COPIES = 3
+MFMA_F16_PEAK_TFLOPS = 2500.0
+PREFILL_FLOP = 3 * 2 * PREFILL_T * HID * DIM  # useful flops of one step
+
+
+def run_prefill(args):
+    """Config 5: X [512 x 4096] fp32 against W_gate|W_up [14336 x 4096] (one
+    qh_gemm_q4_f32_multi launch), then H [512 x 14336] against W_down
+    [4096 x 14336] (qh_gemm_q4_f32): the prefill projections of one MLP, as
+    the reference runs them one token row at a time (model.c:1485-1561).
+    The timed steps run as one captured graph, step i using weight copy
+    i % PREFILL_COPIES (330 MB, past the MALL); inputs resident in HBM."""
+    import qorus_amd as qa
+    from qorus_amd import synthetic as syn
+    lib = qa.lib()
+    rng = syn.rng_for(5555)
+    T = PREFILL_T
+    sets = []
+    for _ in range(PREFILL_COPIES):
+        bufs = [qa.DeviceBuffer.from_numpy(syn.gen_q4(M, N, rng)) for M, N in ((HID, DIM), (HID, DIM), (DIM, HID))]
+        ts = [qa.q4_tensor(b.ptr, M, N) for b, (M, N) in zip(bufs, ((HID, DIM), (HID, DIM), (DIM, HID)))]
+        sets.append((bufs, ts))
+    X = qa.DeviceBuffer.from_numpy(rng.standard_normal((T, DIM), dtype=np.float32))
+    H = qa.DeviceBuffer.from_numpy(rng.standard_normal((T, HID), dtype=np.float32))
+    G, U, Y = qa.DeviceBuffer(T * HID * 4), qa.DeviceBuffer(T * HID * 4), qa.DeviceBuffer(T * DIM * 4)
+    ws_gu = qa.DeviceBuffer(lib.qh_gemm_workspace_bytes(DIM, T, 2 * HID))
+    ws_d = qa.DeviceBuffer(lib.qh_gemm_workspace_bytes(HID, T, DIM))
+    stream = qa.Stream()
+    s = stream.handle
+    ys = ptr_array([G.ptr, U.ptr])
+
+    def gate_up(i):
+        ts = sets[i % PREFILL_COPIES][1]
+        qa.check(lib.qh_gemm_q4_f32_multi(ptr_array([ts[0].addr, ts[1].addr]), ys, 2, X.ptr, T, ws_gu.ptr, s))
+
+    def down(i):
+        ts = sets[i % PREFILL_COPIES][1]
+        qa.check(lib.qh_gemm_q4_f32(ts[2].addr, H.ptr, T, Y.ptr, ws_d.ptr, s))
+
+    def capture(fns, n):
+        qa.check(lib.qh_stream_begin_capture(s))
+        for i in range(n):
+            for f in fns:
+                f(i)
+        g = C.c_void_p()
+        qa.check(lib.qh_stream_end_capture(s, C.byref(g)))
+        return g.value
+
+    steps = max(6, args.steps // 20)
+    warm = capture([gate_up, down], 3)
+    qa.check(lib.qh_graph_launch(warm, s))
+    stream.sync()
+
+    def time_graph(fns):
+        g = capture(fns, steps)
+        a, b = qa.Event(), qa.Event()
+        a.record(stream)
+        qa.check(lib.qh_graph_launch(g, s))
+        b.record(stream)
+        stream.sync()
+        lib.qh_graph_destroy(g)
+        return a.elapsed_ms(b) / steps
+
+    qa.check(lib.qh_device_synchronize())
+    t0 = time.perf_counter()
+    ms_step = time_graph([gate_up, down])
+    wall = time.perf_counter() - t0
+    ms_gu = time_graph([gate_up])
+    ms_d = time_graph([down])
+    lib.qh_graph_destroy(warm)
+    tflops = PREFILL_FLOP / (ms_step * 1e-3) / 1e12
+    cpu = None if args.no_cpu else run_cpu_prefill()
+    return {"workload": "config5: 512-token prefill GEMM, X 512x4096 vs W_gate|W_up 14336x4096 (one launch) then "
+                        "512x14336 vs W_down 4096x14336; one hipGraph of all timed steps, 3 rotated weight copies",
+            "dtype": "q4_0 x f32 on fp16 MFMA (exact q-8 operand, x as fp16 hi + lo*2^11, fp32 accumulate)",
+            "ms_per_step": round(ms_step, 4), "steps": steps, "tokens_per_s": round(T / (ms_step * 1e-3), 1),
+            "useful_flop_per_step": PREFILL_FLOP, "TFLOP_s": round(tflops, 1),
+            "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS,
+            "launch_us": {"gate_up": round(ms_gu * 1e3, 1), "down": round(ms_d * 1e3, 1)},
+            "wall_s": round(wall, 3), "cpu_baseline": cpu}
+
+
+def run_cpu_prefill(rows=12):
+    """Config 5 on one pinned host core as the reference runs it: one
+    q_gemv_q4_f32_avx2 (oracle/_ref) per token row and matrix; a bounded
+    sample of `rows` token rows of each of the three matrices, reported as
+    prefill tokens per second."""
+    from oracle import oracle as orc
+    if not orc.ref_available():
+        return None
+    from qorus_amd import synthetic as syn
+    R = orc.ref()
+    rng = syn.rng_for(5556)
+    mats = []
+    for M, N in ((HID, DIM), (HID, DIM), (DIM, HID)):
+        W = orc.aligned_copy(syn.gen_q4(M, N, rng).reshape(-1))
+        mats.append((W, orc.q4_tensor(W.ctypes.data, M, N), N, orc.aligned_empty((M,), np.float32)))
+    xs = {N: orc.aligned_copy(syn.gen_f32(N, rng)) for N in (DIM, HID)}
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        for W, t, N, y in mats:
+            assert R.q_gemv_q4_f32_avx2(C.addressof(t[0]), xs[N].ctypes.data, y.ctypes.data) == 0
+        t0 = time.perf_counter()
+        for _ in range(rows):
+            for W, t, N, y in mats:
+                R.q_gemv_q4_f32_avx2(C.addressof(t[0]), xs[N].ctypes.data, y.ctypes.data)
+        el = time.perf_counter() - t0
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    return {"value": round(rows / el, 3), "unit": "prefill tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"{rows} token rows x 3 matrices of the reference's q_gemv_q4_f32_avx2 on 1 pinned core "
+                      f"({orc.cpu_model_name()})"}
+
+
+# ---------------------------------------------------------------------------
 # HBM traffic of the dominant kernel (rocprofv3 --pmc passes)
 # ---------------------------------------------------------------------------
 COPY_BYTES = 256 << 20
@@ -600,6 +723,7 @@ def main():
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
     ap.add_argument("--no-lmhead", action="store_true", help="skip the config-3 LM-head leg")
     ap.add_argument("--no-sample", action="store_true", help="skip the q_sample_token leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill GEMM leg")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -624,6 +748,7 @@ def main():
     lmhead = None if args.no_lmhead else run_lmhead(args)
     decode = None if args.no_decode else run_decode(args)
     sample = None if args.no_sample else run_sample()
+    prefill = None if args.no_prefill else run_prefill(args)
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -651,6 +776,7 @@ def main():
         "lmhead": lmhead,
         "decode": decode,
         "sample": sample,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
 
