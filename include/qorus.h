@@ -86,6 +86,14 @@ q_error_code q_matmul_f32_avx2(const q_tensor* Q_RESTRICT A,
                                const q_tensor* Q_RESTRICT B, q_tensor* C,
                                q_context* Q_RESTRICT ctx);
 
+/* Causal mask: every element above the diagonal of the square fp32 matrix
+ * scores [n x n] (row stride nb[0]/4 >= n) := mask_value; the rest keeps
+ * its bits.  Same validation order and codes as the reference.  Host
+ * pointers, synchronous (the batched prefill of llama_forward needs no
+ * mask: each query attends exactly the cached keys up to its position).
+ * Replaces reference qorus.h:91-100 / src/ops/avx2/causal_mask_fp32.c:16-138. */
+q_error_code q_causal_mask_f32_avx2(q_tensor* scores, float mask_value);
+
 /* out = a + b (1-D, in-place allowed).
  * Replaces reference qorus.h:109-113 / src/ops/avx2/add_fp32.c:17-164. */
 q_error_code q_add_f32_avx2(const q_tensor* a, const q_tensor* b, q_tensor* output);

@@ -136,12 +136,19 @@ q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const*
 size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total);
 q_error_code qh_gemm_q4_f32(const q_tensor* W, const float* X, uint32_t T, float* Y, void* workspace,
                             qh_stream s);
-/* Two matrices with the same N sharing X (W_gate|W_up of the MLP) in one
- * launch: Ys[i] = X . Ws[i]^T, n in {1, 2}. */
+/* Up to three matrices with the same N sharing X (Wq|Wk|Wv of attention,
+ * W_gate|W_up of the MLP) in one launch: Ys[i] = X . Ws[i]^T, n in {1, 2, 3}. */
 q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, uint32_t n, const float* X,
                                   uint32_t T, void* workspace, qh_stream s);
 
 /* ---- Vector ops (device pointers, same validation as the qorus.h op) ---- */
+
+/* Device form of q_causal_mask_f32_avx2 (reference
+ * src/ops/avx2/causal_mask_fp32.c:16-138): elements above the diagonal of
+ * the n x n matrix at scores (row stride ld >= n floats) := mask_value.
+ * scores NULL -> INVALID_ARG; n == 0 or ld < n -> INVALID_SIZE; not device
+ * memory covering the n rows -> INVALID_ARG. */
+q_error_code qh_causal_mask_f32(float* scores, uint32_t n, uint32_t ld, float mask_value, qh_stream s);
 
 /* Reference src/ops/avx2/rmsnorm.c:15-92 (sum of squares reduced as a fixed
  * tree; the reference's 8-lane sequential order and rsqrtps seed are not

@@ -158,13 +158,14 @@ def lib():
         L.or_argmax.restype = C.c_uint32
         L.or_add.argtypes = [_f32p, _f32p, _f32p, C.c_uint32]
         L.or_mul.argtypes = [_f32p, _f32p, _f32p, C.c_uint32]
+        L.or_causal_mask.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_float]
         L.or_dot_f32.argtypes = [_f32p, _f32p, C.c_uint32]
         L.or_dot_f32.restype = C.c_float
         L.or_matmul_f32.argtypes = [_f32p, _f32p, _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.or_attention_decode.argtypes = [_f32p, _f32p, _f32p, C.c_uint32, C.c_uint32,
                                           C.c_uint32, C.c_uint32, C.c_uint32]
         L.or_gemm_q4_rows.argtypes = [_u8p, C.c_uint32, C.c_uint32, _f32p, C.c_uint32, _f32p]
-        L.or_decode_step.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, _f32p]
+        L.or_decode_step.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
         L.or_decode_step.restype = C.c_uint32
         L.or_sample_token.argtypes = [C.c_void_p, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_int, C.c_int,
                                       C.POINTER(C.c_uint64)]
@@ -261,6 +262,8 @@ def ref():
         R.q_mul_f32_avx2.restype = C.c_int
         R.q_matmul_f32_avx2.argtypes = [C.c_void_p] * 4
         R.q_matmul_f32_avx2.restype = C.c_int
+        R.q_causal_mask_f32_avx2.argtypes = [C.c_void_p, C.c_float]
+        R.q_causal_mask_f32_avx2.restype = C.c_int
         R.q_alloc_arena.argtypes = [C.c_void_p, C.c_size_t]
         R.q_alloc_arena.restype = C.c_int
         R.q_free_memory.argtypes = [C.c_void_p]
@@ -357,6 +360,13 @@ def mul(a, b):
     a, b = f32(a), f32(b)
     o = np.empty_like(a)
     lib().or_mul(a, b, o, a.size)
+    return o
+
+
+def causal_mask(m: np.ndarray, n: int, v: float) -> np.ndarray:
+    """or_causal_mask on a copy of m [n][ld] (row stride ld = m.shape[1])."""
+    o = np.ascontiguousarray(m, dtype=np.float32).copy()
+    lib().or_causal_mask(o.reshape(-1), n, o.shape[1], v)
     return o
 
 
@@ -478,6 +488,21 @@ def ref_matmul(A, B):
     rc = R.q_matmul_f32_avx2(C.addressof(ta), C.addressof(tb), C.addressof(tc), C.addressof(ctx))
     R.q_free_memory(C.addressof(ctx))
     return rc, Cm.copy()
+
+
+def ref_causal_mask(m: np.ndarray, v: float, ne=None, dtype=Q_F32, offset: int = 0):
+    """Reference q_causal_mask_f32_avx2 on a copy of m [rows][ld] (32-byte
+    aligned plus `offset` bytes); ne defaults to (rows, rows).  Returns
+    (rc, matrix)."""
+    R = ref()
+    rows, ld = m.shape
+    raw = aligned_empty((rows * ld + 16,), np.float32, 64)
+    o = raw[offset // 4: offset // 4 + rows * ld].reshape(rows, ld)
+    o[...] = m
+    ne = ne or (rows, rows)
+    t, k = make_tensor(o.ctypes.data, (ne[0], ne[1], 1, 1), (ld * 4, 4, 4, 4), dtype)
+    rc = R.q_causal_mask_f32_avx2(C.addressof(t), C.c_float(v))
+    return rc, o.copy()
 
 
 class _RefModel(C.Structure):
@@ -620,8 +645,12 @@ class DecodeOracle:
 
     def step(self, token: int, pos: int):
         logits = np.empty(self.h["vocab"], dtype=np.float32)
-        tok = lib().or_decode_step(C.addressof(self.m), token, pos, logits)
+        tok = lib().or_decode_step(C.addressof(self.m), token, pos, logits.ctypes.data)
         return int(tok), logits
+
+    def fill(self, token: int, pos: int):
+        """The step's cache rows only (no LM head)."""
+        lib().or_decode_step(C.addressof(self.m), token, pos, None)
 
 
 def cpu_model_name() -> str:

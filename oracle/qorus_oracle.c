@@ -40,6 +40,10 @@
  *                      memory (ties at a cut keep lower indices; no filter
  *                      keeps every token) have no reference fixture.
  *   or_add/mul         bit-equality with oracle/_ref.
+ *   or_causal_mask     bit-equality with oracle/_ref's q_causal_mask_f32_avx2
+ *                      (every seq_len 1..70 and 255/256/257, row stride n and
+ *                      n + 8, NaN payloads below the diagonal and in the
+ *                      stride padding); brute-force index rule.
  *   or_dot_f32/matmul  bit-equality with oracle/_ref's q_matmul_f32_avx2.
  *   or_attention_decode  composition of the above; fp64 textbook attention
  *                      (with the polynomial exp) within tolerance.
@@ -471,6 +475,15 @@ void or_mul(const float* a, const float* b, float* out, uint32_t N) {
     for (uint32_t i = 0; i < N; i++) out[i] = a[i] * b[i];
 }
 
+/* Reference src/ops/avx2/causal_mask_fp32.c:53-135: in row i of the n x n
+ * matrix (row stride ld floats) every column j > i becomes v; the blend of
+ * the boundary block selects by index (j > i), so the other elements keep
+ * their bits, NaN payloads included; columns n .. ld-1 are not touched. */
+void or_causal_mask(float* m, uint32_t n, uint32_t ld, float v) {
+    for (uint32_t i = 0; i < n; i++)
+        for (uint32_t j = i + 1; j < n; j++) m[(size_t)i * ld + j] = v;
+}
+
 /* ------------------------------------------------------------------------ */
 /* FP32 dot in the order of reference src/ops/avx2/matmul_fp32.c:339-453:
  * for K&~31 elements four 8-lane FMA accumulators (element k feeds
@@ -590,9 +603,12 @@ uint32_t or_decode_step(const or_model* m, uint32_t token, uint32_t pos, float* 
         or_gemv_q4(m->w_down[l], dim, hid, mm, a);
         or_add(x1, a, x, dim);
     }
-    or_rmsnorm(x, m->output_norm, h, dim, m->eps);
-    or_gemv_q4(m->lm_head, m->vocab, dim, h, logits);
-    const uint32_t tok = or_argmax(logits, m->vocab);
+    uint32_t tok = 0;
+    if (logits) {  /* NULL: the cache rows only (a prompt's earlier tokens) */
+        or_rmsnorm(x, m->output_norm, h, dim, m->eps);
+        or_gemv_q4(m->lm_head, m->vocab, dim, h, logits);
+        tok = or_argmax(logits, m->vocab);
+    }
     free(x); free(h); free(q); free(qr); free(k); free(v); free(o); free(a);
     free(x1); free(g); free(u); free(gs); free(mm); free(cs); free(sn);
     return tok;

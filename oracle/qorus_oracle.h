@@ -55,6 +55,7 @@ uint32_t or_sample_token(const float* logits, uint32_t V, float temperature, uin
                          int logits_aligned, int nucleus_all, uint64_t* state);
 void or_add(const float* a, const float* b, float* out, uint32_t N);
 void or_mul(const float* a, const float* b, float* out, uint32_t N);
+void or_causal_mask(float* m, uint32_t n, uint32_t ld, float v);
 /* Dot product in the order of q_matmul_f32_avx2's inner loop. */
 float or_dot_f32(const float* a, const float* b, uint32_t K);
 /* C[M x N] = A[M x K] . B[K x N] (row-major, dense). */

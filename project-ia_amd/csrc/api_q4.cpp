@@ -228,10 +228,10 @@ size_t qh_gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
 q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, uint32_t n, const float* X,
                                   uint32_t T, void* workspace, qh_stream s) {
     if (!Ws) return Q_ERR_INVALID_ARG;
-    if (n < 1 || n > 2) return Q_ERR_INVALID_SIZE;
-    const uint8_t* w[2];
-    float* y[2];
-    uint32_t M[2];
+    if (n < 1 || n > 3) return Q_ERR_INVALID_SIZE;
+    const uint8_t* w[3];
+    float* y[3];
+    uint32_t M[3];
     uint32_t M_total = 0;
     for (uint32_t i = 0; i < n; ++i) {
         const q_tensor* W = Ws[i];

@@ -169,6 +169,46 @@ q_error_code q_matmul_f32_avx2(const q_tensor* __restrict__ A, const q_tensor* _
     return Q_OK;
 }
 
+// Reference src/ops/avx2/causal_mask_fp32.c:16-138, validation in its
+// order: NULL scores or data -> INVALID_ARG; ne[0] == 0 or ne[0] != ne[1] ->
+// INVALID_SIZE; type != F32 -> INVALID_DTYPE; data not 32-byte aligned ->
+// MISALIGNED; n == 1 -> OK (nothing above the diagonal); row stride
+// nb[0]/4 < n -> INVALID_SIZE.  The n rows are staged through HBM and come
+// back whole (only the strict upper triangle changes).
+q_error_code q_causal_mask_f32_avx2(q_tensor* scores, float mask_value) {
+    if (!scores || !scores->data) return Q_ERR_INVALID_ARG;
+    const uint32_t n = scores->ne[0];
+    if (n == 0 || n != scores->ne[1]) return Q_ERR_INVALID_SIZE;
+    if (scores->type != Q_F32) return Q_ERR_INVALID_DTYPE;
+    if (!aligned(scores->data, 32)) return Q_ERR_MISALIGNED;
+    if (n == 1) return Q_OK;
+    const size_t ld = scores->nb[0] / sizeof(float);
+    if (ld < n) return Q_ERR_INVALID_SIZE;
+    Device* d;
+    QH_TRY_CODE(device(&d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    Stager st;
+    QH_TRY_CODE(st.open(d, Stager::round((size_t)n * n * 4)));
+    float* dm = st.take((size_t)n * n);
+    hipStream_t s = d->stream;
+    float* hm = static_cast<float*>(scores->data);
+    QH_TRY(hipMemcpy2DAsync(dm, (size_t)n * 4, hm, ld * 4, (size_t)n * 4, n, hipMemcpyHostToDevice, s));
+    QH_TRY(launch_causal_mask(dm, n, n, mask_value, s));
+    QH_TRY(hipMemcpy2DAsync(hm, ld * 4, dm, (size_t)n * 4, (size_t)n * 4, n, hipMemcpyDeviceToHost, s));
+    QH_TRY(hipStreamSynchronize(s));
+    return Q_OK;
+}
+
+q_error_code qh_causal_mask_f32(float* scores, uint32_t n, uint32_t ld, float mask_value, qh_stream s) {
+    if (!scores) return Q_ERR_INVALID_ARG;
+    if (n == 0 || ld < n) return Q_ERR_INVALID_SIZE;
+    if (n == 1) return Q_OK;
+    if (!device_range(scores, ((size_t)(n - 1) * ld + n) * 4))
+        return fail(hipErrorInvalidValue, "qh_causal_mask_f32: scores is not device memory of n rows");
+    QH_TRY(launch_causal_mask(scores, n, ld, mask_value, (hipStream_t)s));
+    return Q_OK;
+}
+
 q_error_code q_rmsnorm_f32_avx2(const float* __restrict__ x, const float* __restrict__ weight,
                                 float* __restrict__ output, uint32_t N, float eps) {
     QH_TRY_CODE(validate_rmsnorm(x, weight, output, N));

@@ -39,6 +39,7 @@
 #include <cstdint>
 
 #include "qh_kernels.hpp"
+#include "qh_vec.hpp"
 
 namespace qh {
 
@@ -61,20 +62,42 @@ __device__ __forceinline__ constexpr int perm8(int p) { return (p >> 1) + 4 * (p
 // X preparation: one workgroup per (padded) token row.
 // xh/xl: [T_pad][N_pad] fp16 (hi, lo), permuted within groups of 8; columns
 // >= N and rows >= T are zero.  meta[t] = (2^-e, non-finite flag).
+// The row fed to the matrix cores is one of
+//   x                      (plain),
+//   (x * r) * norm_w       (RMSNorm, r = rms_scale of the row: the decode
+//                           prologue's factor, reference rmsnorm.c:33-89),
+//   silu(x) * u            (the SwiGLU product, reference silu.c:75-82 then
+//                           mul_fp32.c; x is the gate row, u the up row).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X, uint32_t T, uint32_t N,
-                                                    uint32_t N_pad, _Float16* __restrict__ xh,
-                                                    _Float16* __restrict__ xl, float2* __restrict__ meta) {
+struct GemmXIn {
+    const float* x;
+    const float* u;       // SwiGLU mode when non-null
+    const float* norm_w;  // RMSNorm mode when non-null
+    float eps;
+};
+
+__global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T, uint32_t N, uint32_t N_pad,
+                                                    _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                    float2* __restrict__ meta) {
     __shared__ float red_m[4];
     __shared__ int red_f[4];
     const uint32_t t = blockIdx.x;
-    const bool valid = t < T;
-    const float* xr = X + (size_t)t * N;
+    const bool valid = t < T;  // uniform over the workgroup
+    const float* xr = in.x + (size_t)t * N;
+    const float* ur = in.u ? in.u + (size_t)t * N : nullptr;
+    float r = 1.0f;
+    if (valid && in.norm_w) r = rms_scale<256>(xr, N, in.eps, red_m);
+    auto value = [&](uint32_t k) -> float {
+        const float v = xr[k];
+        if (ur) return silu_approx(v) * ur[k];
+        if (in.norm_w) return (v * r) * in.norm_w[k];
+        return v;
+    };
     float m = 0.0f;
     int nf = 0;
     if (valid) {
         for (uint32_t i = threadIdx.x; i < N; i += 256) {
-            const float v = xr[i];
+            const float v = value(i);
             nf |= !__builtin_isfinite(v);
             m = fmaxf(m, fabsf(v));
         }
@@ -104,7 +127,7 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X,
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
             const uint32_t k = g * 8 + (uint32_t)perm8(p);
-            const float v = (valid && !nf && k < N) ? ldexpf(xr[k], e) : 0.0f;
+            const float v = (valid && !nf && k < N) ? ldexpf(value(k), e) : 0.0f;
             const _Float16 h = (_Float16)v;
             hv[p] = h;
             lv[p] = (_Float16)((v - (float)h) * 2048.0f);  // exact difference, exact scaling
@@ -118,11 +141,14 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const float* __restrict__ X,
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
+constexpr int kGemmMaxSeg = 3;
+
 struct GemmArgs {
-    const uint8_t* w[2];
-    float* y[2];
-    uint32_t M[2];
-    uint32_t mt_end[2];   // cumulative m-tile counts per segment
+    const uint8_t* w[kGemmMaxSeg];
+    float* y[kGemmMaxSeg];
+    const float* res[kGemmMaxSeg];  // optional residual rows added to y (same layout)
+    uint32_t M[kGemmMaxSeg];
+    uint32_t mt_end[kGemmMaxSeg];   // cumulative m-tile counts per segment
     uint32_t nseg;
     uint32_t nblk;        // blocks per weight row
     uint32_t T;
@@ -136,8 +162,26 @@ struct GemmArgs {
     const float2* meta;
     float* part;          // [split][T][M_total-slot] partials (split > 1)
     uint32_t part_ld;     // partial row length (sum of segment M)
-    uint32_t part_off[2]; // column offset of each segment in a partial row
+    uint32_t part_off[kGemmMaxSeg];  // column offset of each segment in a partial row
 };
+
+// Segment of m-tile index mt / of partial-row column c.
+__device__ __forceinline__ uint32_t seg_of_tile(const GemmArgs& a, uint32_t mt) {
+    return (a.nseg > 1 && mt >= a.mt_end[0] ? 1u : 0u) + (a.nseg > 2 && mt >= a.mt_end[1] ? 1u : 0u);
+}
+__device__ __forceinline__ uint32_t seg_of_col(const GemmArgs& a, uint32_t c) {
+    return (a.nseg > 1 && c >= a.part_off[1] ? 1u : 0u) + (a.nseg > 2 && c >= a.part_off[2] ? 1u : 0u);
+}
+
+// Final value of Y[t][m] in segment sg from the fp32 sum v of the scaled
+// operands: v * 2^-e, plus the residual when given; NaN for a non-finite row.
+__device__ __forceinline__ void gemm_store(const GemmArgs& a, uint32_t sg, uint32_t t, uint32_t m, float v) {
+    const float2 mt = a.meta[t];
+    const size_t i = (size_t)t * a.M[sg] + m;
+    float y = v * mt.x;
+    if (a.res[sg]) y = a.res[sg][i] + y;
+    a.y[sg][i] = mt.y != 0.0f ? __builtin_nanf("") : y;
+}
 
 // 8 nibbles of one dword -> 8 fp16 (q - 8), in the kPerm order.
 __device__ __forceinline__ h8v unpack8(uint32_t w) {
@@ -182,8 +226,8 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         if (mm >= n_mt) return;
     }
     const uint32_t mtile = mm / a.split, sp = mm % a.split;
-    const uint32_t sg = (a.nseg > 1 && mtile >= a.mt_end[0]) ? 1u : 0u;
-    const uint32_t m0 = (mtile - (sg ? a.mt_end[0] : 0u)) * BM;
+    const uint32_t sg = seg_of_tile(a, mtile);
+    const uint32_t m0 = (mtile - (sg ? a.mt_end[sg - 1] : 0u)) * BM;
     const uint32_t t0 = tt * BT;
     const uint32_t M = a.M[sg];
     const uint32_t row_bytes = a.nblk * 20u;
@@ -321,8 +365,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                     if (a.split > 1) {
                         a.part[((size_t)sp * a.T + t) * a.part_ld + a.part_off[sg] + m] = v[r];
                     } else {
-                        const float2 mt = a.meta[t];
-                        a.y[sg][(size_t)t * M + m] = mt.y != 0.0f ? __builtin_nanf("") : v[r] * mt.x;
+                        gemm_store(a, sg, t, m, v[r]);
                     }
                 }
             }
@@ -338,10 +381,8 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
         const uint32_t t = (uint32_t)(i / ld), c = (uint32_t)(i % ld);
         float v = a.part[i];
         for (uint32_t sp = 1; sp < a.split; ++sp) v += a.part[(size_t)sp * n + i];
-        const uint32_t sg = (a.nseg > 1 && c >= a.part_off[1]) ? 1u : 0u;
-        const uint32_t m = c - a.part_off[sg];
-        const float2 mt = a.meta[t];
-        a.y[sg][(size_t)t * a.M[sg] + m] = mt.y != 0.0f ? __builtin_nanf("") : v * mt.x;
+        const uint32_t sg = seg_of_col(a, c);
+        gemm_store(a, sg, t, c - a.part_off[sg], v);
     }
 }
 
@@ -373,9 +414,11 @@ size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
     return b;
 }
 
-hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t* M, int nseg, uint32_t N,
-                       const float* X, uint32_t T, void* ws, hipStream_t s) {
-    if (nseg < 1 || nseg > 2 || T == 0 || N == 0 || N % 32 != 0) return hipErrorInvalidValue;
+hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipStream_t s) {
+    const uint32_t N = in.N, T = in.T;
+    const int nseg = sg.n;
+    if (nseg < 1 || nseg > kGemmMaxSeg || T == 0 || N == 0 || N % 32 != 0 || !in.x) return hipErrorInvalidValue;
+    if (in.norm_w && in.u) return hipErrorInvalidValue;
     const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
     uint8_t* p = static_cast<uint8_t*>(ws);
     const size_t plane = align256((size_t)tp * np * 2);
@@ -387,13 +430,14 @@ hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t*
     uint32_t mt = 0, mtot = 0;
     for (int i = 0; i < nseg; ++i) {
         // Weight offsets are 32-bit buffer offsets.
-        if ((uint64_t)M[i] * (N / 32u) * 20u >= (1ull << 31)) return hipErrorInvalidValue;
-        a.w[i] = w[i];
-        a.y[i] = y[i];
-        a.M[i] = M[i];
+        if (sg.M[i] == 0 || (uint64_t)sg.M[i] * (N / 32u) * 20u >= (1ull << 31)) return hipErrorInvalidValue;
+        a.w[i] = sg.w[i];
+        a.y[i] = sg.y[i];
+        a.res[i] = sg.res[i];
+        a.M[i] = sg.M[i];
         a.part_off[i] = mtot;
-        mtot += M[i];
-        mt += (M[i] + kGemmBM - 1) / kGemmBM;
+        mtot += sg.M[i];
+        mt += (sg.M[i] + kGemmBM - 1) / kGemmBM;
         a.mt_end[i] = mt;
     }
     a.nseg = (uint32_t)nseg;
@@ -407,7 +451,8 @@ hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t*
     a.part_ld = mtot;
     // The XCD-aware order needs the token-tile count to divide the 8 XCDs.
     a.xcd_map = (8u % a.n_tt == 0) ? 1u : 0u;
-    hipLaunchKernelGGL(k_gemm_xprep, dim3(tp), dim3(256), 0, s, X, T, N, np, const_cast<_Float16*>(a.xh),
+    const GemmXIn xin{in.x, in.u, in.norm_w, in.eps};
+    hipLaunchKernelGGL(k_gemm_xprep, dim3(tp), dim3(256), 0, s, xin, T, N, np, const_cast<_Float16*>(a.xh),
                        const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -420,6 +465,23 @@ hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t*
     const uint32_t rg = (uint32_t)std::min<size_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(k_gemm_reduce, dim3(rg), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t* M, int nseg, uint32_t N,
+                       const float* X, uint32_t T, void* ws, hipStream_t s) {
+    if (nseg < 1 || nseg > kGemmMaxSeg) return hipErrorInvalidValue;
+    GemmSegs sg{};
+    sg.n = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        sg.w[i] = w[i];
+        sg.y[i] = y[i];
+        sg.M[i] = M[i];
+    }
+    GemmRows in{};
+    in.x = X;
+    in.T = T;
+    in.N = N;
+    return launch_gemm_ex(sg, in, ws, s);
 }
 
 }  // namespace qh

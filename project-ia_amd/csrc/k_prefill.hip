@@ -1,0 +1,300 @@
+// k_prefill.hip -- batched-prefill kernels for gfx950 other than the GEMM:
+// token embedding rows, RoPE of the Q|K rows with the KV-cache stores, and
+// the causal attention of T queries over the cache on fp32 matrix cores.
+//
+// The prefill computes what T successive decode steps compute (reference
+// src/models/model.c:1655-1850 run with seq_len = 1 per token): token t at
+// position pos0 + t attends the cached keys 0 .. pos0 + t.  (The reference's
+// own seq_len > 1 branch normalizes only the first row, model.c:1108 and
+// 1624, and attends only within the batch, model.c:1340-1440; a prompt
+// continued at pos0 > 0 then ignores its cached keys.  This build keeps the
+// token-by-token result for every seq_len.)
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qh_prefill.hpp"
+#include "qh_vec.hpp"
+
+namespace qh {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kPHd = 128;  // head_dim the prefill kernels are written for
+
+__global__ __launch_bounds__(256) void k_embed_rows(const float* __restrict__ embd, const uint32_t* __restrict__ tok,
+                                                    uint32_t dim, float* __restrict__ X) {
+    const uint32_t t = blockIdx.y;
+    const float4* src = reinterpret_cast<const float4*>(embd + (size_t)tok[t] * dim);
+    float4* dst = reinterpret_cast<float4*>(X + (size_t)t * dim);
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < dim / 4; i += gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_embed_rows(const float* embd, const uint32_t* tok, uint32_t T, uint32_t dim, float* X,
+                             hipStream_t s) {
+    if (T == 0 || dim == 0 || dim % 4 != 0) return hipErrorInvalidValue;
+    const uint32_t gx = (dim / 4 + 255) / 256;
+    hipLaunchKernelGGL(k_embed_rows, dim3(gx, T), dim3(256), 0, s, embd, tok, dim, X);
+    return hipGetLastError();
+}
+
+// RoPE pair (x0, x1) -> (x0*c - x1*s, x1*c + x0*s), reference
+// src/ops/avx2/rope.c:244-285 with the table of position pos0 + t.
+__device__ __forceinline__ float2 rope_pair(float2 x, float c, float sn) {
+    const float a0 = x.x * c, b0 = x.y * sn;
+    const float a1 = x.y * c, b1 = x.x * sn;
+    return make_float2(a0 - b0, a1 + b1);
+}
+
+__global__ __launch_bounds__(256) void k_rope_kv_rows(float* __restrict__ Q, const float* __restrict__ K,
+                                                      const float* __restrict__ V, const float* __restrict__ ct,
+                                                      const float* __restrict__ st, uint32_t pos0,
+                                                      uint32_t n_heads, uint32_t n_kv, uint32_t max_seq,
+                                                      float* __restrict__ kv_layer) {
+    const uint32_t t = blockIdx.x, P = pos0 + t;
+    const uint32_t qd = n_heads * kPHd, kvd = n_kv * kPHd;
+    const float* c = ct + (size_t)P * kPHd;
+    const float* sn = st + (size_t)P * kPHd;
+    float* q = Q + (size_t)t * qd;
+    for (uint32_t p = threadIdx.x; p < qd / 2; p += 256) {
+        const uint32_t i = 2 * p, e = i % kPHd;
+        float2* qp = reinterpret_cast<float2*>(q + i);
+        *qp = rope_pair(*qp, c[e], sn[e]);
+    }
+    const float* k = K + (size_t)t * kvd;
+    const float* v = V + (size_t)t * kvd;
+    for (uint32_t p = threadIdx.x; p < kvd / 2; p += 256) {
+        const uint32_t i = 2 * p, h = i / kPHd, e = i % kPHd;
+        float* dst = kv_layer + ((size_t)h * max_seq + P) * 2 * kPHd;
+        *reinterpret_cast<float2*>(dst + e) = rope_pair(*reinterpret_cast<const float2*>(k + i), c[e], sn[e]);
+        *reinterpret_cast<float2*>(dst + kPHd + e) = *reinterpret_cast<const float2*>(v + i);
+    }
+}
+
+hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const float* cos_tab,
+                               const float* sin_tab, uint32_t pos0, uint32_t T, uint32_t n_heads, uint32_t n_kv,
+                               uint32_t max_seq, float* kv_layer, hipStream_t s) {
+    if (T == 0 || n_kv == 0 || (uint64_t)pos0 + T > max_seq) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rope_kv_rows, dim3(T), dim3(256), 0, s, Q, K, V, cos_tab, sin_tab, pos0, n_heads, n_kv,
+                       max_seq, kv_layer);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Causal prefill attention on v_mfma_f32_16x16x4_f32.
+//
+// Workgroup: 16 queries (a query tile) x the G query heads of one KV head,
+// one wave per head; the G waves share the key/value rows, staged in LDS 64
+// keys at a time.  Per query (as in the decode step): s_j = (q . k_j) *
+// scale for j <= P (its position), m = max_j s_j, e_j = exp_approx(s_j - m)
+// for j < (P+1) & ~7 and expf above (all expf when P+1 < 8), o = sum_j e_j v_j
+// times 1/sum_j e_j (divided by the sum when P+1 < 8).  The polynomial exp
+// is not multiplicative, so the max is found in a first pass over the keys
+// and the scores are recomputed (bit-identically) in the second.
+//
+// Fragment layouts (16x16x4: lane l feeds A[l%16][l/16] and B[l/16][l%16];
+// D[4*(l/16)+r][l%16] lands in register r of lane l):
+//  * scores S^T[key][query] = K . Q^T: the contraction index of MFMA step kk
+//    in lane group g = l/16 is element 32g + kk of the head (any pairing of
+//    the 128 elements to the 32 steps x 4 groups works when A and B agree),
+//    so each lane reads 32 consecutive floats of one K row and keeps 32
+//    consecutive floats of its query;
+//  * the result gives lane l query l%16 and keys 4g + r of the 16-key
+//    block, which is exactly lane l's A fragment of O = P . V for step kk = r
+//    if step kk pairs lane group g with key 4g + kk; V is read in that key
+//    order, and output column d of tile t in lane l%16 is 4*(l%16) + t
+//    (t < 4) or 64 + 4*(l%16) + t - 4, so every lane reads and writes
+//    float4s.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
+constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
+
+template <uint32_t G>
+__global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a) {
+    constexpr uint32_t NT = 64 * G;
+    constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
+    static_assert(kLoads * NT == kAttnKS * (kPHd / 4), "stage/thread mismatch");
+    __shared__ __attribute__((aligned(16))) float lk[kAttnKS][kAttnRS];
+    __shared__ __attribute__((aligned(16))) float lv[kAttnKS][kAttnRS];
+
+    const uint32_t n_qt = (a.T + 15) / 16;
+    const uint32_t qt = n_qt - 1 - blockIdx.x;  // the longest rows first
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t t0 = qt * 16;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t h = kvh * G + (threadIdx.x >> 6);
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    const uint32_t t_last = min(t0 + 15u, a.T - 1u);
+    const uint32_t n_keys = a.pos0 + t_last + 1u;  // keys of the tile's last query
+    const uint32_t n_stages = (n_keys + kAttnKS - 1) / kAttnKS;
+    const size_t q_ld = (size_t)a.n_heads * kPHd;
+    const float* kbase = a.kv + (size_t)kvh * a.max_seq * 2 * kPHd;
+
+    // This lane's query (B column li) and its 32 elements 32*lg .. 32*lg+31.
+    const uint32_t my_t = t0 + li;
+    const bool q_ok = my_t < a.T;
+    const uint32_t P = a.pos0 + my_t;  // attends keys 0..P
+    const uint32_t S = P + 1u;
+    const uint32_t Sv = S >= 8u ? (S & ~7u) : 0u;
+    float qv[32];
+    {
+        const float4* qr = reinterpret_cast<const float4*>(a.q + (size_t)(q_ok ? my_t : t_last) * q_ld +
+                                                           (size_t)h * kPHd + 32 * lg);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 v = qr[c];
+            qv[4 * c + 0] = q_ok ? v.x : 0.0f;
+            qv[4 * c + 1] = q_ok ? v.y : 0.0f;
+            qv[4 * c + 2] = q_ok ? v.z : 0.0f;
+            qv[4 * c + 3] = q_ok ? v.w : 0.0f;
+        }
+    }
+
+    // Rows st*KS .. +KS-1 of K (and V) into LDS; rows past the tile's keys
+    // repeat its last key (in bounds; masked by j <= P below).
+    auto stage = [&](uint32_t st, bool with_v) {
+        float4 kr[kLoads], vr[kLoads];
+#pragma unroll
+        for (uint32_t u = 0; u < kLoads; ++u) {
+            const uint32_t i = threadIdx.x + u * NT;
+            const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
+            uint32_t j = st * kAttnKS + r;
+            j = j < n_keys ? j : n_keys - 1u;
+            const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)j * 2 * kPHd) + c;
+            kr[u] = src[0];
+            if (with_v) vr[u] = src[kPHd / 4];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kLoads; ++u) {
+            const uint32_t i = threadIdx.x + u * NT;
+            const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
+            *reinterpret_cast<float4*>(&lk[r][4 * c]) = kr[u];
+            if (with_v) *reinterpret_cast<float4*>(&lv[r][4 * c]) = vr[u];
+        }
+    };
+
+    // Scores of keys sub*16 .. sub*16+15 of the staged block (times scale
+    // applied by the caller): two accumulation chains, then their sum.
+    auto scores = [&](uint32_t sub) -> f4v {
+        f4v d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* kr = &lk[sub * 16 + li][32 * lg];
+#pragma unroll
+        for (int c = 0; c < 8; c += 2) {
+            const float4 k0 = *reinterpret_cast<const float4*>(kr + 4 * c);
+            const float4 k1 = *reinterpret_cast<const float4*>(kr + 4 * c + 4);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.x, qv[4 * c + 0], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.x, qv[4 * c + 4], d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.y, qv[4 * c + 1], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.y, qv[4 * c + 5], d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.z, qv[4 * c + 2], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.z, qv[4 * c + 6], d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.w, qv[4 * c + 3], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.w, qv[4 * c + 7], d1, 0, 0, 0);
+        }
+        return d0 + d1;
+    };
+
+    // ---- pass 1: row max ----
+    float mx = -INFINITY;
+    for (uint32_t st = 0; st < n_stages; ++st) {
+        __syncthreads();  // the previous stage's reads are done
+        stage(st, false);
+        __syncthreads();
+#pragma unroll
+        for (uint32_t sub = 0; sub < kAttnKS / 16; ++sub) {
+            const uint32_t jb = st * kAttnKS + sub * 16;
+            if (jb >= n_keys) break;
+            const f4v d = scores(sub);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t j = jb + 4 * lg + r;
+                const float sc = d[r] * a.scale;
+                if (q_ok && j <= P) mx = fmaxf(mx, sc);
+            }
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+
+    // ---- pass 2: e_j, their sum and P.V ----
+    f4v acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    float sum = 0.0f;
+    for (uint32_t st = 0; st < n_stages; ++st) {
+        __syncthreads();
+        stage(st, true);
+        __syncthreads();
+#pragma unroll
+        for (uint32_t sub = 0; sub < kAttnKS / 16; ++sub) {
+            const uint32_t jb = st * kAttnKS + sub * 16;
+            if (jb >= n_keys) break;
+            const f4v d = scores(sub);
+            float e[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t j = jb + 4 * lg + r;
+                const float dd = d[r] * a.scale - mx;
+                float ev = 0.0f;
+                if (q_ok && j <= P) ev = (j < Sv) ? exp_approx(dd) : expf(dd);
+                e[r] = ev;
+                sum += ev;
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float* vr = &lv[sub * 16 + 4 * lg + kk][0];
+                const float4 v0 = *reinterpret_cast<const float4*>(vr + 4 * li);
+                const float4 v1 = *reinterpret_cast<const float4*>(vr + 64 + 4 * li);
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.x, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.y, acc[1], 0, 0, 0);
+                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.z, acc[2], 0, 0, 0);
+                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.w, acc[3], 0, 0, 0);
+                acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.x, acc[4], 0, 0, 0);
+                acc[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.y, acc[5], 0, 0, 0);
+                acc[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.z, acc[6], 0, 0, 0);
+                acc[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.w, acc[7], 0, 0, 0);
+            }
+        }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+
+    // ---- output: register r of lane l is query 4*(l/16) + r ----
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = 4 * lg + (uint32_t)r;
+        const float total = __shfl(sum, (int)i);  // lane i holds query i's sum
+        const uint32_t t = t0 + i;
+        if (t < a.T) {
+            const bool small = a.pos0 + t + 1u < 8u;
+            const float inv = 1.0f / total;
+            float o[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[c] = small ? acc[c][r] / total : acc[c][r] * inv;
+            float* dst = a.o + (size_t)t * q_ld + (size_t)h * kPHd;
+            *reinterpret_cast<float4*>(dst + 4 * li) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4*>(dst + 64 + 4 * li) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+    }
+}
+
+template <uint32_t G>
+static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
+    const uint32_t n_qt = (a.T + 15) / 16;
+    hipLaunchKernelGGL(k_prefill_attn<G>, dim3(n_qt, a.n_kv), dim3(64 * G), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
+    if (a.T == 0 || a.n_kv == 0 || a.n_heads % a.n_kv != 0 || (uint64_t)a.pos0 + a.T > a.max_seq)
+        return hipErrorInvalidValue;
+    switch (a.n_heads / a.n_kv) {
+        case 1: return run_prefill_attention<1>(a, s);
+        case 2: return run_prefill_attention<2>(a, s);
+        case 4: return run_prefill_attention<4>(a, s);
+        case 8: return run_prefill_attention<8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace qh

@@ -69,6 +69,22 @@ hipError_t launch_rope(const float* x, const float* ct, const float* st, float* 
     return hipGetLastError();
 }
 
+// Causal mask (reference src/ops/avx2/causal_mask_fp32.c:16-138): every
+// element above the diagonal of the n x n matrix (row stride ld floats) is
+// set to mask_value; the diagonal, the lower triangle and the columns past n
+// keep their bits.  One workgroup per row, float stores only.
+__global__ __launch_bounds__(256) void k_causal_mask(float* __restrict__ m, uint32_t n, uint32_t ld, float v) {
+    const uint32_t i = blockIdx.x;
+    float* row = m + (size_t)i * ld;
+    for (uint32_t j = i + 1u + threadIdx.x; j < n; j += 256) row[j] = v;
+}
+
+hipError_t launch_causal_mask(float* m, uint32_t n, uint32_t ld, float mask_value, hipStream_t s) {
+    if (n < 2) return hipSuccess;
+    hipLaunchKernelGGL(k_causal_mask, dim3(n - 1), dim3(256), 0, s, m, n, ld, mask_value);
+    return hipGetLastError();
+}
+
 // SiLU (reference src/ops/avx2/silu.c:44-91).  With u != nullptr the output
 // is silu(x)*u, the SwiGLU product of reference src/models/model.c:1516-1549.
 __global__ __launch_bounds__(256) void k_silu(const float* __restrict__ x, const float* __restrict__ u,

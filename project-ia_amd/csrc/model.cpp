@@ -21,12 +21,14 @@
 
 #include <cmath>
 #include <cstdint>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
 
 #include "qh_decode.hpp"
 #include "qh_kernels.hpp"
+#include "qh_prefill.hpp"
 #include "qh_runtime.hpp"
 #include "qh_sample.hpp"
 
@@ -67,6 +69,15 @@ struct ModelPlan {
     void* sample_ws = nullptr;               // device workspace of sampled generation
     uint32_t* pinned = nullptr;              // host staging for token/pos
     float* pinned_logits = nullptr;          // host staging for the logits llama_forward returns
+    // Batched prefill (llama_forward with seq_len > 1), allocated at its
+    // first use: row buffers for pf_rows tokens and the GEMM workspace.
+    uint8_t* pf_arena = nullptr;
+    uint32_t pf_rows = 0;
+    float *pf_x = nullptr, *pf_x1 = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    float *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr;
+    uint32_t* pf_tok = nullptr;
+    void* pf_ws = nullptr;
+    uint32_t* pinned_tok = nullptr;          // host staging for a chunk's tokens
 };
 
 static std::mutex g_plan_mu;
@@ -80,6 +91,8 @@ void plan_destroy(CtxState* st) {
     if (p->gen_graph) (void)hipGraphExecDestroy(p->gen_graph);
     if (p->arena) (void)hipFree(p->arena);
     if (p->sample_ws) (void)hipFree(p->sample_ws);
+    if (p->pf_arena) (void)hipFree(p->pf_arena);
+    if (p->pinned_tok) (void)hipHostFree(p->pinned_tok);
     if (p->pinned) (void)hipHostFree(p->pinned);
     if (p->pinned_logits) (void)hipHostFree(p->pinned_logits);
     if (p->stream) (void)hipStreamDestroy(p->stream);
@@ -318,6 +331,158 @@ static q_error_code capture(ModelPlan* p, bool feedback, hipGraphExec_t* out) {
     (void)hipGraphDestroy(g);
     if (e3 != hipSuccess) return fail(e3, "hipGraphInstantiate");
     return Q_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Batched prefill: T tokens at positions pos0 .. pos0+T-1 through every layer
+// as GEMMs on the matrix cores, the same result as T decode steps (see
+// k_prefill.hip).  Per layer: Q|K|V = W . RMSNorm(X) (the norm made where the
+// GEMM converts its rows), RoPE + KV-cache stores, causal attention over the
+// cache, X1 = X + Wo . O, G|U = W . RMSNorm(X1), X = X1 + W_down .
+// (silu(G) * U) (the SwiGLU product made where the GEMM converts its rows).
+// The last chunk ends with the LM head of its last row.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPrefillRows = 512;  // tokens per prefill chunk
+
+static size_t prefill_ws_bytes(const ModelPlan* p, uint32_t T) {
+    const q_llama_config& c = p->cfg;
+    size_t b = gemm_workspace_bytes(c.dim, T, c.dim + 2 * p->kvd);
+    b = std::max(b, gemm_workspace_bytes(c.dim, T, c.dim));
+    b = std::max(b, gemm_workspace_bytes(c.dim, T, 2 * c.hidden_dim));
+    b = std::max(b, gemm_workspace_bytes(c.hidden_dim, T, c.dim));
+    return b;
+}
+
+static q_error_code prefill_alloc(ModelPlan* p) {
+    if (p->pf_arena) return Q_OK;
+    const q_llama_config& c = p->cfg;
+    const uint32_t R = std::min(kPrefillRows, c.max_seq_len);
+    size_t ws = 0;
+    for (uint32_t T = 1; T <= R; ++T) ws = std::max(ws, prefill_ws_bytes(p, T));
+    size_t bytes = 0;
+    auto carve = [&](size_t b) {
+        const size_t at = bytes;
+        bytes += (b + 255) & ~(size_t)255;
+        return at;
+    };
+    const size_t rd = (size_t)R * c.dim * 4, rk = (size_t)R * p->kvd * 4, rh = (size_t)R * c.hidden_dim * 4;
+    const size_t o_x = carve(rd), o_x1 = carve(rd), o_q = carve(rd), o_k = carve(rk), o_v = carve(rk);
+    const size_t o_o = carve(rd), o_g = carve(rh), o_u = carve(rh), o_t = carve((size_t)R * 4), o_ws = carve(ws);
+    if (!p->pinned_tok)
+        QH_TRY(hipHostMalloc(reinterpret_cast<void**>(&p->pinned_tok), (size_t)R * 4, hipHostMallocDefault));
+    QH_TRY(hipMalloc(&p->pf_arena, bytes));
+    uint8_t* A = p->pf_arena;
+    p->pf_x = reinterpret_cast<float*>(A + o_x);
+    p->pf_x1 = reinterpret_cast<float*>(A + o_x1);
+    p->pf_q = reinterpret_cast<float*>(A + o_q);
+    p->pf_k = reinterpret_cast<float*>(A + o_k);
+    p->pf_v = reinterpret_cast<float*>(A + o_v);
+    p->pf_o = reinterpret_cast<float*>(A + o_o);
+    p->pf_g = reinterpret_cast<float*>(A + o_g);
+    p->pf_u = reinterpret_cast<float*>(A + o_u);
+    p->pf_tok = reinterpret_cast<uint32_t*>(A + o_t);
+    p->pf_ws = A + o_ws;
+    p->pf_rows = R;
+    return Q_OK;
+}
+
+static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool last) {
+    const q_llama_config& c = p->cfg;
+    hipStream_t s = p->stream;
+    hipError_t e;
+#define QH_E(x)                          \
+    do {                                 \
+        e = (x);                         \
+        if (e != hipSuccess) return e;   \
+    } while (0)
+    QH_E(launch_embed_rows(p->embd, p->pf_tok, T, c.dim, p->pf_x, s));
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const LayerDev& L = p->layers[l];
+        float* kvl = p->kv + (size_t)l * p->kv_layer_floats;
+        GemmSegs qkv;
+        qkv.n = 3;
+        qkv.w[0] = L.wq;
+        qkv.w[1] = L.wk;
+        qkv.w[2] = L.wv;
+        qkv.y[0] = p->pf_q;
+        qkv.y[1] = p->pf_k;
+        qkv.y[2] = p->pf_v;
+        qkv.M[0] = c.dim;
+        qkv.M[1] = qkv.M[2] = p->kvd;
+        GemmRows xn;
+        xn.x = p->pf_x;
+        xn.norm_w = L.attn_norm;
+        xn.eps = c.rms_norm_eps;
+        xn.T = T;
+        xn.N = c.dim;
+        QH_E(launch_gemm_ex(qkv, xn, p->pf_ws, s));
+        QH_E(launch_rope_kv_rows(p->pf_q, p->pf_k, p->pf_v, p->cos_tab, p->sin_tab, pos0, T, c.n_heads,
+                                 c.n_kv_heads, c.max_seq_len, kvl, s));
+        PrefillAttnArgs aa;
+        aa.q = p->pf_q;
+        aa.kv = kvl;
+        aa.o = p->pf_o;
+        aa.T = T;
+        aa.pos0 = pos0;
+        aa.n_heads = c.n_heads;
+        aa.n_kv = c.n_kv_heads;
+        aa.max_seq = c.max_seq_len;
+        aa.scale = p->scale;
+        QH_E(launch_prefill_attention(aa, s));
+        GemmSegs wo;
+        wo.n = 1;
+        wo.w[0] = L.wo;
+        wo.y[0] = p->pf_x1;
+        wo.res[0] = p->pf_x;
+        wo.M[0] = c.dim;
+        GemmRows on;
+        on.x = p->pf_o;
+        on.T = T;
+        on.N = c.dim;
+        QH_E(launch_gemm_ex(wo, on, p->pf_ws, s));
+        GemmSegs gu;
+        gu.n = 2;
+        gu.w[0] = L.wg;
+        gu.w[1] = L.wu;
+        gu.y[0] = p->pf_g;
+        gu.y[1] = p->pf_u;
+        gu.M[0] = gu.M[1] = c.hidden_dim;
+        GemmRows x1n;
+        x1n.x = p->pf_x1;
+        x1n.norm_w = L.ffn_norm;
+        x1n.eps = c.rms_norm_eps;
+        x1n.T = T;
+        x1n.N = c.dim;
+        QH_E(launch_gemm_ex(gu, x1n, p->pf_ws, s));
+        GemmSegs wd;
+        wd.n = 1;
+        wd.w[0] = L.wd;
+        wd.y[0] = p->pf_x;
+        wd.res[0] = p->pf_x1;
+        wd.M[0] = c.dim;
+        GemmRows hn;
+        hn.x = p->pf_g;
+        hn.u = p->pf_u;
+        hn.T = T;
+        hn.N = c.hidden_dim;
+        QH_E(launch_gemm_ex(wd, hn, p->pf_ws, s));
+    }
+    if (last) {
+        // LM head of RMSNorm(last row), as in the decode step.
+        const float* xr = p->pf_x + (size_t)(T - 1) * c.dim;
+        GemvSeg lm{p->lm_head, p->logits, nullptr, c.vocab_size};
+        if (p->fused) {
+            GemvDecode dn;
+            dn.norm_w = p->out_norm;
+            dn.eps = c.rms_norm_eps;
+            QH_E(launch_gemv_f32(&lm, 1, c.dim, xr, nullptr, s, &dn));
+        } else {
+            QH_E(launch_xprep(xr, c.dim, p->out_norm, c.rms_norm_eps, nullptr, p->xd_a, s));
+            QH_E(launch_gemv(&lm, 1, c.dim / 32, p->xd_a, s));
+        }
+    }
+#undef QH_E
+    return hipSuccess;
 }
 
 static ModelPlan* plan_of(const q_llama_model* model, q_context* ctx) {
@@ -584,8 +749,10 @@ void llama_free_graph(q_llama_model* __restrict__ model) {
 }
 
 // Reference src/models/model.c:1655-1850: tokens[0..seq_len) at positions
-// pos.., logits of the last token copied to the host buffer `logits`.
-// Tokens run one decode step each (causal attention over the cache).
+// pos.., logits of the last token copied to the host buffer `logits`, the KV
+// cache filled at pos .. pos+seq_len-1.  One token runs the captured decode
+// step; more run the batched prefill in chunks of up to 512 tokens (the
+// result of one decode step per token: causal attention over the cache).
 q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restrict__ ctx,
                            const uint32_t* __restrict__ tokens, uint32_t seq_len, uint32_t pos,
                            float* __restrict__ logits) {
@@ -603,14 +770,24 @@ q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restr
     if (!p) return Q_ERR_INVALID_ARG;
     QH_TRY_CODE(check_kv(p, ctx));
     QH_TRY_CODE(bind_kv(p, ctx));
-    if (!p->step_graph) QH_TRY_CODE(capture(p, false, &p->step_graph));
-    for (uint32_t t = 0; t < seq_len; ++t) {
+    if (seq_len == 1) {
+        if (!p->step_graph) QH_TRY_CODE(capture(p, false, &p->step_graph));
         QH_TRY(hipStreamSynchronize(p->stream));  // pinned staging is reused each step
-        p->pinned[0] = tokens[t];
-        p->pinned[1] = pos + t;
+        p->pinned[0] = tokens[0];
+        p->pinned[1] = pos;
         QH_TRY(hipMemcpyAsync(p->tok, &p->pinned[0], 4, hipMemcpyHostToDevice, p->stream));
         QH_TRY(hipMemcpyAsync(p->pos, &p->pinned[1], 4, hipMemcpyHostToDevice, p->stream));
         QH_TRY(hipGraphLaunch(p->step_graph, p->stream));
+    } else {
+        QH_TRY_CODE(prefill_alloc(p));
+        for (uint32_t c0 = 0; c0 < seq_len; c0 += p->pf_rows) {
+            const uint32_t T = std::min(p->pf_rows, seq_len - c0);
+            QH_TRY(hipStreamSynchronize(p->stream));  // the token staging is reused per chunk
+            std::memcpy(p->pinned_tok, tokens + c0, (size_t)T * 4);
+            QH_TRY(hipMemcpyAsync(p->pf_tok, p->pinned_tok, (size_t)T * 4, hipMemcpyHostToDevice, p->stream));
+            const hipError_t e = enqueue_prefill(p, T, pos + c0, c0 + T == seq_len);
+            if (e != hipSuccess) return fail(e, "llama_forward: prefill launch");
+        }
     }
     // through pinned memory (one DMA, then a host copy): a pageable copy of
     // the 513 KB Llama-3 logits is several times slower

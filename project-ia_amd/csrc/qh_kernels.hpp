@@ -84,17 +84,39 @@ hipError_t launch_gemv_f32_amax(const GemvSeg& seg, uint32_t N, const float* x, 
                                 uint32_t cap, uint32_t* n_part, hipStream_t s);
 
 // ---- batched prefill GEMM (k_gemm.hip) ----
-// Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 or 2) matrices sharing
+// Y_i[t][m] = sum_k W_i[m][k] X[t][k] for nseg (1 to 3) matrices sharing
 // X [T][N] (row-major fp32); Y_i is [T][M_i].  ws: gemm_workspace_bytes.
 size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total);
 hipError_t launch_gemm(const uint8_t* const* w, float* const* y, const uint32_t* M, int nseg, uint32_t N,
                        const float* X, uint32_t T, void* ws, hipStream_t s);
+// The general form: up to 3 weight matrices, an optional residual per
+// output (Y_i = R_i + W_i . x, R_i may equal Y_i), and the GEMM's rows x
+// taken as X (plain), RMSNorm(X) * norm_w, or silu(X) * U (X the gate
+// rows): the prefill layer's norms and SwiGLU product are made where the
+// rows are converted for the matrix cores.
+struct GemmSegs {
+    int n = 0;
+    const uint8_t* w[3] = {};
+    float* y[3] = {};
+    const float* res[3] = {};
+    uint32_t M[3] = {};
+};
+struct GemmRows {
+    const float* x = nullptr;       // [T][N]
+    const float* u = nullptr;       // SwiGLU mode: [T][N] up rows
+    const float* norm_w = nullptr;  // RMSNorm mode: [N] weight
+    float eps = 0.0f;
+    uint32_t T = 0, N = 0;
+};
+hipError_t launch_gemm_ex(const GemmSegs& segs, const GemmRows& rows, void* ws, hipStream_t s);
 
 // ---- vector kernels (k_vec.hip) ----
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s);
 // RoPE of n_vec consecutive vectors of length N with one cos/sin table pair.
 hipError_t launch_rope(const float* x, const float* ct, const float* st, float* y, uint32_t N,
                        uint32_t n_vec, hipStream_t s);
+// Elements above the diagonal of an n x n matrix (row stride ld) := mask_value.
+hipError_t launch_causal_mask(float* m, uint32_t n, uint32_t ld, float mask_value, hipStream_t s);
 // y = silu(x) (u == nullptr) or silu(x) * u.
 hipError_t launch_silu(const float* x, const float* u, float* y, uint32_t N, hipStream_t s);
 hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s);

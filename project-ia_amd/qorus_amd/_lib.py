@@ -155,6 +155,8 @@ def lib():
     _sig(L, "q_add_f32_avx2", i32, vp, vp, vp)
     _sig(L, "q_matmul_f32_avx2", i32, vp, vp, vp, vp)
     _sig(L, "q_mul_f32_avx2", i32, vp, vp, vp)
+    _sig(L, "q_causal_mask_f32_avx2", i32, vp, f32)
+    _sig(L, "qh_causal_mask_f32", i32, vp, u32, u32, f32, vp)
     _sig(L, "qh_rmsnorm_f32", i32, vp, vp, vp, u32, f32, vp)
     _sig(L, "qh_rope_f32", i32, vp, vp, vp, vp, u32, u32, vp)
     _sig(L, "qh_silu_f32", i32, vp, vp, u32, vp)

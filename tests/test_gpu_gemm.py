@@ -45,9 +45,10 @@ class Gemm:
         if len(self.Ms) == 1:
             qa.check(lib.qh_gemm_q4_f32(self.t[0].addr, self.dX.ptr, self.T, self.dY[0].ptr, self.ws.ptr, None))
         else:
-            Ws = (C.c_void_p * 2)(*[t.addr for t in self.t])
-            Ys = (C.c_void_p * 2)(*[d.ptr for d in self.dY])
-            qa.check(lib.qh_gemm_q4_f32_multi(Ws, Ys, 2, self.dX.ptr, self.T, self.ws.ptr, None))
+            n = len(self.Ms)
+            Ws = (C.c_void_p * n)(*[t.addr for t in self.t])
+            Ys = (C.c_void_p * n)(*[d.ptr for d in self.dY])
+            qa.check(lib.qh_gemm_q4_f32_multi(Ws, Ys, n, self.dX.ptr, self.T, self.ws.ptr, None))
         qa.check(lib.qh_device_synchronize())
         return [d.download(np.float32, (self.T, M)) for d, M in zip(self.dY, self.Ms)]
 
@@ -105,6 +106,13 @@ def test_gemm_multi_equals_single_and_is_deterministic(qa):
     (S1,) = Gemm(qa, [W1], [M1], N, T)(X)
     (S2,) = Gemm(qa, [W2], [M2], N, T)(X)
     assert np.array_equal(Y1, S1) and np.array_equal(Y2, S2)
+    # three matrices (the Q|K|V launch of the prefill: segment boundaries
+    # inside the m-tile sequence at 200 and 336 rows)
+    M3 = 72
+    W3 = orc.gen_q4(M3, N, rng)
+    Q1, Q2, Q3 = Gemm(qa, [W1, W2, W3], [M1, M2, M3], N, T)(X)
+    (S3,) = Gemm(qa, [W3], [M3], N, T)(X)
+    assert np.array_equal(Q1, S1) and np.array_equal(Q2, S2) and np.array_equal(Q3, S3)
 
 
 def test_gemm_scaled_and_nonfinite_rows(qa):
@@ -188,9 +196,9 @@ def test_gemm_api_errors(qa):
     bad.t.type = qa.Q_F32
     assert f(bad.addr, dX.ptr, T, dY.ptr, ws.ptr, None) == -14
     assert lib.qh_gemm_q4_f32_multi(None, None, 1, dX.ptr, T, ws.ptr, None) == -10
-    Ws = (C.c_void_p * 2)(t.addr, t.addr)
-    Ys = (C.c_void_p * 2)(dY.ptr, dY.ptr)
-    assert lib.qh_gemm_q4_f32_multi(Ws, Ys, 3, dX.ptr, T, ws.ptr, None) == -15
+    Ws = (C.c_void_p * 4)(t.addr, t.addr, t.addr, t.addr)
+    Ys = (C.c_void_p * 4)(dY.ptr, dY.ptr, dY.ptr, dY.ptr)
+    assert lib.qh_gemm_q4_f32_multi(Ws, Ys, 4, dX.ptr, T, ws.ptr, None) == -15
     assert f(t.addr, dX.ptr, T, dY.ptr, ws.ptr, None) == 0
     assert lib.qh_device_synchronize() == 0
 

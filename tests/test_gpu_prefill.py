@@ -1,0 +1,202 @@
+"""GPU parity of the batched prefill: llama_forward with seq_len > 1 (every
+projection on the MFMA GEMM with the RMSNorm / SwiGLU product made where it
+converts its rows, RoPE + KV-cache stores, causal attention of the prompt's
+queries over the cache on fp32 matrix cores, chunks of up to 512 tokens)
+against the oracle's token-by-token decode steps (or_decode_step), which is
+what the prefill must equal: token t of the prompt attends the cached keys
+0 .. pos + t.
+
+Bars (the decode step's, written out):
+  * logits of the last token: max |gpu - oracle| <= 1e-4 * max |oracle logit|;
+  * greedy token equal;
+  * every KV-cache row the prompt writes: max |gpu - oracle| <= 1e-4 * max |row|
+    per layer; rows outside the prompt keep their bits;
+  * decode steps after the prefill (reading the prefilled rows) give the
+    oracle's greedy tokens.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def build(qa, tmp_path, h, seed, prefill, name="m.qorus"):
+    path = tmp_path / name
+    qa.synthetic.write_synthetic_model(path, h, seed)
+    m = qa.Model(path)
+    hd = h.dim // h.n_heads
+    rng = orc.rng_for(seed, 99)
+    kv = np.zeros((h.n_layers, h.n_kv, h.max_seq, 2, hd), np.float32)
+    kv[:, :, :prefill] = rng.standard_normal((h.n_layers, h.n_kv, prefill, 2, hd), dtype=np.float32)
+    m.upload_kv(kv)
+    blob = np.fromfile(path, dtype=np.uint8)
+    return m, blob, kv
+
+
+def rel_err(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / np.max(np.abs(b)))
+
+
+def oracle_prompt(ref, toks, pos):
+    for i, t in enumerate(toks[:-1]):
+        ref.fill(t, pos + i)
+    return ref.step(toks[-1], pos + len(toks) - 1)
+
+
+def check_prompt(qa, m, h, kv0, ref, toks, pos, label=""):
+    print(f"prefill {label}: T={len(toks)} pos={pos}", flush=True)
+    lg = m.forward(toks, pos)
+    tok_ref, lg_ref = oracle_prompt(ref, toks, pos)
+    e = rel_err(lg, lg_ref)
+    print(f"  logits rel err {e:.3e}", flush=True)
+    assert e <= 1e-4, (label, e)
+    assert int(np.argmax(lg)) == tok_ref, label
+    kv_gpu = m.download_kv().reshape(kv0.shape)
+    T = len(toks)
+    for l in range(h.n_layers):
+        got = kv_gpu[l, :, pos:pos + T]
+        want = ref.kv[l, :, pos:pos + T]
+        ek = rel_err(got, want)
+        assert ek <= 1e-4, (label, l, ek)
+    # rows outside the prompt keep their bits
+    assert np.array_equal(kv_gpu[:, :, :pos], kv0[:, :, :pos])
+    assert np.array_equal(kv_gpu[:, :, pos + T:], kv0[:, :, pos + T:])
+    return tok_ref
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 1), (8, 1), (16, 2), (2, 2), (8, 2)])
+def test_prefill_gqa_groups(qa, tmp_path, n_heads, n_kv):
+    """GQA groups 4, 8, 8, 1 and 4 (the attention kernel is instantiated per
+    group); a 37-token prompt at position 0 (query tiles of 16: the last one
+    ragged; rows of fewer than 8 keys use the reference's libm exp)."""
+    h = qa.QorusHeader(vocab=700, dim=128 * n_heads, hidden=1024, n_layers=2, n_heads=n_heads, n_kv=n_kv,
+                       max_seq=128)
+    m, blob, kv = build(qa, tmp_path, h, 31 + n_heads + n_kv, 0)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        rng = orc.rng_for(n_heads, n_kv)
+        toks = [int(t) for t in rng.integers(0, h.vocab, 37)]
+        check_prompt(qa, m, h, kv, ref, toks, 0, f"group {n_heads // n_kv}")
+    finally:
+        m.close()
+
+
+def test_prefill_continues_a_cached_context(qa, tmp_path):
+    """A 20-token prompt at position 50 over a random cache: its queries
+    attend the 50 cached keys too (the reference's own seq_len > 1 branch
+    would not); then greedy decode steps read the prefilled rows."""
+    h = qa.QorusHeader(vocab=500, dim=512, hidden=1024, n_layers=2, n_heads=4, n_kv=2, max_seq=128)
+    P = 50
+    m, blob, kv = build(qa, tmp_path, h, 41, P)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(41, 1).integers(0, h.vocab, 20)]
+        tok = check_prompt(qa, m, h, kv, ref, toks, P)
+        n = 6
+        got, _ = m.generate(tok, P + 20, n)
+        want, t = [], tok
+        for i in range(n):
+            t, _ = ref.step(t, P + 20 + i)
+            want.append(t)
+        assert got.tolist() == want
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("T", [2, 8, 9, 16, 17])
+def test_prefill_short_prompts(qa, tmp_path, T):
+    """Prompts of 2 to 17 tokens at position 0: query rows with fewer than 8
+    keys (libm exp, divided by the sum), exactly 8, the first polynomial
+    row, one full and one ragged 16-query tile."""
+    h = qa.QorusHeader(vocab=300, dim=256, hidden=512, n_layers=3, n_heads=2, n_kv=1, max_seq=64)
+    m, blob, kv = build(qa, tmp_path, h, 50 + T, 0)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(50, T).integers(0, h.vocab, T)]
+        check_prompt(qa, m, h, kv, ref, toks, 0, f"T={T}")
+    finally:
+        m.close()
+
+
+def test_prefill_chunks_past_512_tokens(qa, tmp_path):
+    """A 600-token prompt at position 3: a 512-token chunk, then 88 tokens
+    whose queries attend the first chunk's keys from the cache."""
+    h = qa.QorusHeader(vocab=400, dim=256, hidden=512, n_layers=2, n_heads=2, n_kv=1, max_seq=640)
+    m, blob, kv = build(qa, tmp_path, h, 61, 3)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(61, 2).integers(0, h.vocab, 600)]
+        check_prompt(qa, m, h, kv, ref, toks, 3, "600 tokens")
+    finally:
+        m.close()
+
+
+def test_prefill_config4_shapes_two_layers(qa, tmp_path):
+    """BASELINE config-4 widths (d 4096, GQA 32/8 x 128, FFN 14336, vocab
+    128256, theta 500000) with 2 of the 32 layers: a 40-token prompt at
+    position 0 (the Q|K|V launch's three segments, the split-K W_down)."""
+    h = qa.QorusHeader(vocab=128256, dim=4096, hidden=14336, n_layers=2, n_heads=32, n_kv=8, max_seq=256)
+    m, blob, kv = build(qa, tmp_path, h, 71, 0, name="c4.qorus")
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(71, 3).integers(0, h.vocab, 40)]
+        check_prompt(qa, m, h, kv, ref, toks, 0, "config-4 shapes")
+    finally:
+        m.close()
+
+
+def test_prefill_unfused_wide_dim(qa, tmp_path):
+    """d_model 4352 (the decode's generic GEMV layers; the LM head after the
+    prefill takes the separate norm + digits launch), GQA 34/17."""
+    h = qa.QorusHeader(vocab=300, dim=4352, hidden=1024, n_layers=2, n_heads=34, n_kv=17, max_seq=64)
+    m, blob, kv = build(qa, tmp_path, h, 81, 5, name="wide.qorus")
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(81, 4).integers(0, h.vocab, 10)]
+        check_prompt(qa, m, h, kv, ref, toks, 5, "wide")
+    finally:
+        m.close()
+
+
+def test_causal_mask_entry_points(qa):
+    """q_causal_mask_f32_avx2 (host) and qh_causal_mask_f32 (device) against
+    or_causal_mask bit for bit, with the reference's validation codes."""
+    import ctypes as C
+    lib = qa.lib()
+    for n, ld in [(1, 1), (2, 2), (7, 7), (9, 17), (64, 64), (257, 264)]:
+        rng = orc.rng_for(n, ld)
+        m = rng.standard_normal((n, ld)).astype(np.float32)
+        if n > 2:
+            m.view(np.uint32)[n - 1, 0] = 0x7FC01234
+        want = orc.causal_mask(m, n, -1e9)
+        # host form
+        h = orc.aligned_copy(m)
+        t, keep = orc.make_tensor(h.ctypes.data, (n, n, 1, 1), (ld * 4, 4, 4, 4), orc.Q_F32)
+        assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1e9) == 0
+        assert np.array_equal(h.view(np.uint32), want.view(np.uint32)), (n, ld)
+        # device form
+        d = qa.DeviceBuffer.from_numpy(m)
+        qa.check(lib.qh_causal_mask_f32(d.ptr, n, ld, -1e9, None))
+        qa.check(lib.qh_device_synchronize())
+        got = d.download(np.float32, (n, ld))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, ld)
+    m = orc.aligned_copy(np.zeros((4, 4), np.float32))
+    mk = lambda ne, dt=orc.Q_F32, ptr=m.ctypes.data, ld=4: orc.make_tensor(ptr, (ne[0], ne[1], 1, 1),
+                                                                             (ld * 4, 4, 4, 4), dt)
+    assert lib.q_causal_mask_f32_avx2(None, -1.0) == -10
+    t, k = mk((4, 8))
+    assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1.0) == -15
+    t, k = mk((0, 0))
+    assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1.0) == -15
+    t, k = mk((4, 4), orc.Q_Q4_0)
+    assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1.0) == -14
+    t, k = mk((4, 4), ptr=m.ctypes.data + 4)
+    assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1.0) == -13
+    t, k = mk((8, 8))
+    assert lib.q_causal_mask_f32_avx2(C.addressof(t), -1.0) == -15
+    assert lib.qh_causal_mask_f32(None, 4, 4, -1.0, None) == -10
+    d = qa.DeviceBuffer(64)
+    assert lib.qh_causal_mask_f32(d.ptr, 4, 3, -1.0, None) == -15
+    assert lib.qh_causal_mask_f32(d.ptr, 16, 16, -1.0, None) == -10  # 1 KB of rows, a 64-byte buffer

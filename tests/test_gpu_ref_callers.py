@@ -26,7 +26,7 @@ CALLERS = REPO / "oracle" / "_ref" / "callers"
 CALLERS_REF = REPO / "oracle" / "_ref" / "callers_ref"
 NAMES = ["test_matmul", "test_matmul_adversarial", "test_ops", "test_dequantize", "test_dequantize_adversarial",
          "test_matmul_f32", "test_add_f32", "test_mul_f32", "test_rmsnorm_adversarial", "test_rope_adversarial",
-         "test_silu_adversarial", "test_softmax_adversarial", "test_main"]
+         "test_silu_adversarial", "test_softmax_adversarial", "test_causal_mask_f32", "test_main"]
 
 
 COUNTS = re.compile(r"Tests (Passed|Failed|Crashed):\s+(\d+)")

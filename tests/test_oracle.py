@@ -250,6 +250,50 @@ def test_add_mul_vs_reference_build():
     assert rc == 0 and same_bits(orc.mul(a, b), r)
 
 
+def _mask_input(n, ld, seed):
+    rng = orc.rng_for(39, seed)
+    m = rng.standard_normal((n, ld)).astype(np.float32)
+    # NaN payloads below the diagonal and in the stride padding must survive
+    bits = m.view(np.uint32)
+    if n > 2:
+        bits[n - 1, 0] = 0x7FC01234
+    if ld > n:
+        bits[0, n] = 0x7F812345
+    return m
+
+
+@needs_ref
+def test_causal_mask_vs_reference_build():
+    for n in list(range(1, 71)) + [255, 256, 257]:
+        for ld in (n, n + 8):
+            m = _mask_input(n, ld, n * 1000 + ld)
+            rc, r = orc.ref_causal_mask(m, -1e9)
+            assert rc == 0
+            o = orc.causal_mask(m, n, -1e9)
+            assert np.array_equal(o.view(np.uint32), r.view(np.uint32)), (n, ld)
+            # brute-force index rule
+            i, j = np.indices((n, ld))
+            up = (j > i) & (j < n)
+            assert np.all(o[up] == np.float32(-1e9))
+            assert np.array_equal(o.view(np.uint32)[~up], m.view(np.uint32)[~up])
+
+
+@needs_ref
+def test_causal_mask_reference_validation_codes():
+    """The codes the device entry points must reproduce (reference
+    causal_mask_fp32.c:20-49): non-square and zero size -> INVALID_SIZE,
+    Q4_0 type -> INVALID_DTYPE, misaligned data -> MISALIGNED, stride below
+    n -> INVALID_SIZE, n == 1 -> OK untouched."""
+    m = _mask_input(4, 4, 1)
+    assert orc.ref_causal_mask(m, -1.0, ne=(4, 8))[0] == -15
+    assert orc.ref_causal_mask(m, -1.0, ne=(0, 0))[0] == -15
+    assert orc.ref_causal_mask(m, -1.0, dtype=orc.Q_Q4_0)[0] == -14
+    assert orc.ref_causal_mask(m, -1.0, offset=4)[0] == -13
+    assert orc.ref_causal_mask(m, -1.0, ne=(8, 8))[0] == -15  # stride 4 < 8
+    rc, r = orc.ref_causal_mask(m[:1, :1], -1.0)
+    assert rc == 0 and r[0, 0] == m[0, 0]
+
+
 def test_argmax_first_index_on_ties():
     x = np.array([1, 5, 5, 2, 5], np.float32)
     assert orc.argmax(x) == 1
