@@ -285,6 +285,7 @@ def run_decode(args):
             m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
             m.upload_kv(kv)
             _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
+        prefill = None if args.no_prompt else run_prompt(m, h)
         m.close()
         avg_ctx = DEC_POS + 1 + (steps - 1) / 2
         bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
@@ -300,12 +301,51 @@ def run_decode(args):
                "sampled_tok_s": None if ms_s is None else round(1e3 / ms_s, 1),
                "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
                                    "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
+        if prefill is not None:
+            out["prefill_512"] = prefill
         if not args.no_cpu:
             out["cpu_baseline"], out["first_token_matches_cpu"] = run_cpu_decode(path, kv, first_tok, int(toks[0]),
                                                                                 args.cpu_decode_tokens)
         return out
     finally:
         shutil.rmtree(d, ignore_errors=True)
+
+
+PROMPT_T = 512
+
+
+def prompt_flop(n_layers=32, T=PROMPT_T):
+    """Useful flops of a T-token prompt through llama_forward: 2*T per weight
+    of the 32 layers (Q|K|V, Wo, W_gate|W_up, W_down) plus the causal
+    attention (q.k and p.v over keys 0..t of each query, 32 heads x 128) and
+    the LM head of the last token."""
+    d, hid, v, kvd = 4096, 14336, 128256, 1024
+    w = d * d * 2 + 2 * kvd * d + 3 * hid * d
+    attn = 2 * 2 * 32 * 128 * (T * (T + 1) // 2)
+    return n_layers * (2 * T * w + attn) + 2 * v * d
+
+
+def run_prompt(m, h, reps=3):
+    """llama_forward of a 512-token prompt at position 0 on the 32-layer
+    model (the batched prefill), wall clock around the synchronous call."""
+    rng = np.random.default_rng(2026)
+    toks = [int(t) for t in rng.integers(0, h.vocab, PROMPT_T)]
+    m.forward(toks, 0)  # first call allocates the prefill buffers
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        m.forward(toks, 0)
+        times.append(time.perf_counter() - t0)
+    ms = 1e3 * sum(times) / len(times)
+    fl = prompt_flop()
+    log(f"[bench] prompt: {PROMPT_T} tokens in {ms:.2f} ms ({PROMPT_T / ms * 1e3:.0f} tok/s)")
+    return {"tokens": PROMPT_T, "ms": round(ms, 3), "tok_s": round(PROMPT_T / ms * 1e3, 1), "reps": reps,
+            "useful_tflop_s": round(fl / (ms * 1e-3) / 1e12, 1),
+            "frac_of_fp16_mfma_peak": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "workload": "llama_forward(512 tokens, pos 0) on the config-4 model (32 layers, Llama-3-8B shape, "
+                        "Q4_0): every projection an MFMA GEMM, causal fp32-MFMA attention, KV rows 0..511 "
+                        "written, LM head of the last token; wall clock of the synchronous call incl. the "
+                        "token upload and the 513 KB logits download"}
 
 
 def run_cpu_decode(path, kv, first_tok, gpu_tok0, n_tokens):
@@ -724,6 +764,8 @@ def main():
     ap.add_argument("--no-lmhead", action="store_true", help="skip the config-3 LM-head leg")
     ap.add_argument("--no-sample", action="store_true", help="skip the q_sample_token leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill GEMM leg")
+    ap.add_argument("--no-prompt", action="store_true",
+                    help="skip the 512-token llama_forward prompt on the config-4 model")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
