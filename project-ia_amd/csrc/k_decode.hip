@@ -8,9 +8,10 @@
 // exp (libm-style expf on the N%8 tail), o_h = sum_j p_j v_j.  Because the
 // polynomial exp is not multiplicative (exp_approx(a+b) != exp_approx(a) *
 // exp_approx(b)), online-softmax rescaling would change results; the max is
-// found first.  Three phases, keys split in chunks of kChunk:
-//   A  scores + per-chunk max           grid (chunks, kv heads)
-//   B  e_j, per-chunk sums and P.V sums  grid (chunks, kv heads)
+// found first.  Three phases:
+//   A  scores + per-chunk max            grid (64-key chunks, kv heads)
+//   B  e_j, per-chunk sums and P.V sums  grid (256-key chunks, kv heads,
+//                                        32-column slices of V)
 //   C  combine + digit prep of o (the Wo GEMV input), one lane per element.
 // KV layout is the reference's [L][kv_head][max_seq][K|V][head_dim].
 #include <hip/hip_runtime.h>
@@ -39,6 +40,46 @@ constexpr uint32_t kMaxGroup = 8;  // q heads per kv head (1, 2, 4 or 8)
 template <int kCtrl>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// The partner across lane bit 2 (lane ^ 4) on DPP: row_shl:4 reads lane + 4,
+// row_shr:4 lane - 4.
+__device__ __forceinline__ float dpp_xor4(float v) {
+    const float up = dpp_f<0x104>(v), dn = dpp_f<0x114>(v);
+    return (threadIdx.x & 4) ? dn : up;
+}
+
+// Max over the wave, the same value in every lane: quads, half rows and rows
+// on DPP (every pairing is exact for a max), then the 4 rows by readlane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// Sum over aligned groups of N consecutive lanes (N <= 32) on DPP (a
+// cross-row step for N = 32); the group's first lane holds the sum in a
+// fixed order (other lanes may hold it in another).
+template <uint32_t N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) v += dpp_f<0xB1>(v);
+    if constexpr (N >= 4) v += dpp_f<0x4E>(v);
+    if constexpr (N >= 8) v += dpp_xor4(v);
+    if constexpr (N >= 16) v += dpp_f<0x128>(v);  // row_ror:8 (lane ^ 8 within a row)
+    if constexpr (N >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+// Sum over the wave in a fixed order (rows on DPP, then the 4 rows in order).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
 }
 
 __device__ __forceinline__ float dot_tree8(float s) {
@@ -132,9 +173,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     // max is exact, so any combination order gives the same result.
 #pragma unroll
     for (uint32_t h = 0; h < group; ++h) {
-        float m = (l == 0) ? mx[h] : -INFINITY;
-#pragma unroll
-        for (int off = 8; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float m = wave_max((l == 0) ? mx[h] : -INFINITY);
         if (lane == 0) smax[wave][h] = m;
     }
     __syncthreads();
@@ -145,6 +184,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     }
 }
 
+// Phase B over 256-key chunks, each split in 4 workgroups by 32-column
+// slices of V (288 workgroups at context 2048, each reading 256 rows of 128
+// bytes): the combine then sums at most 32 partials, one round of loads.
+constexpr uint32_t kPvChunk = 256;
+constexpr uint32_t kPvSlices = kHd / 32;
+
 template <uint32_t group>
 __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ scores, const float* __restrict__ kv,
                                                  const uint32_t* __restrict__ pos_p,
@@ -152,90 +197,102 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ score
                                                  const float* __restrict__ part_max, uint32_t n_chunks,
                                                  float* __restrict__ part_sum, float* __restrict__ o_part) {
     const uint32_t S = *pos_p + 1u;
-    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y;
-    const uint32_t j0 = chunk * kChunk;
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, sl = blockIdx.z;
+    const uint32_t j0 = chunk * kPvChunk;
     if (j0 >= S) return;
-    const uint32_t nch = (S + kChunk - 1) / kChunk;
-    const uint32_t Sv = S >= 8 ? (S & ~7u) : 0u;  // polynomial exp below Sv, expf above
-    __shared__ float e_s[kMaxGroup][kChunk];
-    __shared__ float o_s[kMaxGroup][kHd];
+    const uint32_t nch = (S + kChunk - 1) / kChunk;  // score chunks holding part_max
+    const uint32_t Sv = S >= 8 ? (S & ~7u) : 0u;     // polynomial exp below Sv, expf above
+    constexpr uint32_t kThr = 32 / group;            // threads per output float4 in the final sum
+    __shared__ __attribute__((aligned(16))) float e_s[group][kPvChunk];
+    __shared__ float4 red[32][group][8];
     __shared__ float gmax[kMaxGroup];
     const uint32_t tid = threadIdx.x;
-    // Loads that do not depend on the global max are issued first: this
-    // chunk's V rows (thread (hf, d): keys hf*32 .. hf*32+31, element d) and
-    // its scores.  Keys past S read a clamped, in-bounds row and are zeroed.
-    const uint32_t d = tid % kHd, hf = tid / kHd;
-    const float* vbase = kv + (size_t)kvh * head_stride + kHd;
-    float vv[32];
+    const uint32_t r = tid >> 3, q = tid & 7;  // rows r, r+32, ..; float4 q of the 32-column slice
+    // Loads that do not depend on the global max first: this thread's 8 V
+    // pieces (rows past S read row S-1, in bounds; their e is 0) and the
+    // chunk's scores.
+    const float* vbase = kv + (size_t)kvh * head_stride + kHd + 32 * sl + 4 * q;
+    float4 vv[8];
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
-        const uint32_t j = j0 + hf * 32 + (uint32_t)u;
-        const float v = vbase[(size_t)(j < S ? j : S - 1u) * (2 * kHd) + d];
-        vv[u] = (j < S) ? v : 0.0f;
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t j = j0 + r + 32u * (uint32_t)k;
+        vv[k] = *reinterpret_cast<const float4*>(vbase + (size_t)(j < S ? j : S - 1u) * (2 * kHd));
     }
-    constexpr uint32_t kPer = (group * kChunk + 255) / 256;
-    float scv[kPer];
+    float scv[group];
+    const uint32_t jt = j0 + tid;
 #pragma unroll
-    for (uint32_t r = 0; r < kPer; ++r) {
-        const uint32_t i = tid + 256 * r;
-        const uint32_t h = i / kChunk, jj = i % kChunk, j = j0 + jj;
-        const bool ok = i < group * kChunk && j < S;
-        const uint32_t hc = h < group ? h : 0u;
-        const float sv = scores[(size_t)(kvh * group + hc) * max_seq + (j < S ? j : S - 1u)];
-        scv[r] = ok ? sv : 0.0f;
-    }
+    for (uint32_t h = 0; h < group; ++h)
+        scv[h] = scores[(size_t)(kvh * group + h) * max_seq + (jt < S ? jt : S - 1u)];
     // Global max per head: one wave per head (lane-strided loads, then a
-    // butterfly max); exact, so the order does not matter.
-    {
-        const uint32_t wv = tid >> 6, ln = tid & 63;
+    // wave max); exact, so the order does not matter.
+    const uint32_t wv = tid >> 6, ln = tid & 63;
+    for (uint32_t hh = wv; hh < group; hh += 4) {
+        const uint32_t h = kvh * group + hh;
+        float m = -INFINITY;
+        for (uint32_t c = ln; c < nch; c += 64) m = fmaxf(m, part_max[(size_t)h * n_chunks + c]);
+        m = wave_max(m);
+        if (ln == 0) gmax[hh] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t h = 0; h < group; ++h) {
+        float e = 0.0f;
+        if (jt < S) {
+            const float dd = scv[h] - gmax[h];
+            e = (jt < Sv) ? exp_approx(dd) : expf(dd);
+        }
+        e_s[h][tid] = e;
+    }
+    __syncthreads();
+    // The chunk's sums (slice 0): lane ln adds keys 4ln..4ln+3 in order, then
+    // a fixed-order wave sum.
+    if (sl == 0) {
         for (uint32_t hh = wv; hh < group; hh += 4) {
-            const uint32_t h = kvh * group + hh;
-            float m = -INFINITY;
-            for (uint32_t c = ln; c < nch; c += 64) m = fmaxf(m, part_max[(size_t)h * n_chunks + c]);
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-            if (ln == 0) gmax[hh] = m;
+            const float4 e4 = *reinterpret_cast<const float4*>(&e_s[hh][4 * ln]);
+            const float sum = wave_sum(((e4.x + e4.y) + e4.z) + e4.w);
+            if (ln == 0) part_sum[(size_t)(kvh * group + hh) * n_chunks + chunk] = sum;
         }
     }
-    __syncthreads();
-    // e_j for the chunk's keys and all group heads.
+    // P.V over this thread's 8 rows for every head of the group.
+    float4 acc[group];
 #pragma unroll
-    for (uint32_t r = 0; r < kPer; ++r) {
-        const uint32_t i = tid + 256 * r;
-        if (i < group * kChunk) {
-            const uint32_t h = i / kChunk, jj = i % kChunk, j = j0 + jj;
-            float e = 0.0f;
-            if (j < S) {
-                const float dd = scv[r] - gmax[h];
-                e = (j < Sv) ? exp_approx(dd) : expf(dd);
-            }
-            e_s[h][jj] = e;
+    for (uint32_t h = 0; h < group; ++h) acc[h] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t jj = r + 32u * (uint32_t)k;
+#pragma unroll
+        for (uint32_t h = 0; h < group; ++h) {
+            const float e = e_s[h][jj];
+            acc[h].x = fmaf(e, vv[k].x, acc[h].x);
+            acc[h].y = fmaf(e, vv[k].y, acc[h].y);
+            acc[h].z = fmaf(e, vv[k].z, acc[h].z);
+            acc[h].w = fmaf(e, vv[k].w, acc[h].w);
         }
     }
+#pragma unroll
+    for (uint32_t h = 0; h < group; ++h) red[r][h][q] = acc[h];
     __syncthreads();
-    if (tid < group) {
-        float sum = 0.0f;
-        for (int jj = 0; jj < kChunk; ++jj) sum += e_s[tid][jj];
-        part_sum[(size_t)(kvh * group + tid) * n_chunks + chunk] = sum;
+    // Sum over the 32 row groups: output float4 (h, q) by kThr consecutive
+    // threads, each over `group` row groups in order, then a lane-group sum.
+    {
+        const uint32_t o = tid / kThr, sub = tid % kThr;
+        const uint32_t h = o >> 3, qq = o & 7u;
+        float4 v = red[sub * group][h][qq];
+#pragma unroll
+        for (uint32_t i = 1; i < group; ++i) {
+            const float4 w = red[sub * group + i][h][qq];
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        v.x = group_sum<kThr>(v.x);
+        v.y = group_sum<kThr>(v.y);
+        v.z = group_sum<kThr>(v.z);
+        v.w = group_sum<kThr>(v.w);
+        if (sub == 0)
+            *reinterpret_cast<float4*>(o_part + ((size_t)chunk * n_heads + kvh * group + h) * kHd + 32 * sl + 4 * qq) = v;
     }
-    // P.V partials: thread (half, d) over its 32 keys, all group heads.
-    float acc[group];
-#pragma unroll
-    for (uint32_t h = 0; h < group; ++h) acc[h] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < 32; ++u) {
-        const int jj = (int)hf * 32 + u;
-#pragma unroll
-        for (uint32_t h = 0; h < group; ++h) acc[h] = fmaf(e_s[h][jj], vv[u], acc[h]);
-    }
-    if (hf == 1)
-#pragma unroll
-        for (uint32_t h = 0; h < group; ++h) o_s[h][d] = acc[h];
-    __syncthreads();
-    if (hf == 0)
-#pragma unroll
-        for (uint32_t h = 0; h < group; ++h)
-            o_part[((size_t)chunk * n_heads + kvh * group + h) * kHd + d] = acc[h] + o_s[h][d];
 }
 
 // o = (sum_c o_part[c]) * (1 / sum_c part_sum[c]) (for S < 8, the reference's
@@ -248,7 +305,7 @@ __global__ __launch_bounds__(kCombThreads) void k_attn_combine(const float* __re
                                                       uint32_t n_chunks, float* __restrict__ o_out,
                                                       uint32_t pad, uint32_t* __restrict__ xd) {
     const uint32_t S = *pos_p + 1u;
-    const uint32_t nch = (S + kChunk - 1) / kChunk;
+    const uint32_t nch = (S + kPvChunk - 1) / kPvChunk;
     const uint32_t t = blockIdx.x * kCombThreads + threadIdx.x;  // element of o
     const uint32_t N = n_heads * kHd;
     const bool valid = t < N;
@@ -296,7 +353,8 @@ static hipError_t run_attention(const AttnArgs& a, hipStream_t s) {
                        a.n_heads, a.max_seq, a.scale, a.scores, a.part_max, n_chunks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_pv<group>, grid, dim3(256), 0, s, a.scores, a.kv_layer, a.pos, head_stride,
+    const dim3 grid_pv((a.max_seq + kPvChunk - 1) / kPvChunk, a.n_kv, kPvSlices);
+    hipLaunchKernelGGL(k_attn_pv<group>, grid_pv, dim3(256), 0, s, a.scores, a.kv_layer, a.pos, head_stride,
                        a.n_heads, a.max_seq, a.part_max, n_chunks, a.part_sum, a.o_part);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
