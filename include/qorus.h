@@ -12,9 +12,8 @@
  * The stream-ordered device entry points used by the on-device decode step
  * are declared in qorus_hip.h.
  *
- * Out of scope for this build (declared nowhere, so a caller fails at link
- * time rather than at run time): the BPE tokenizer (reference qorus.h:230-273)
- * and q_generate (reference qorus.h:318-320).
+ * The BPE tokenizer and q_generate are host code around the device path
+ * (text in, token ids to the model, ids back to text).
  */
 #ifndef QORUS_H
 #define QORUS_H
@@ -149,6 +148,42 @@ q_error_code llama_forward(q_llama_model* Q_RESTRICT model, q_context* Q_RESTRIC
 q_error_code q_sample_token(const float* Q_RESTRICT logits, uint32_t vocab_size,
                             float temperature, uint32_t top_k, float top_p,
                             uint32_t* Q_RESTRICT token_id_out, q_context* Q_RESTRICT ctx);
+
+/* Autoregressive generation: the prompt through llama_forward at position 0
+ * (the batched prefill), then per step q_sample_token on the last logits
+ * (with state->ctx's arena), the token stored, a stop at the tokenizer's EOS
+ * or a full context, and the token through llama_forward at the next
+ * position.  Same validation order and codes as the reference; the arena is
+ * reset before each forward, as there.  (qh_llama_generate_sampled in
+ * qorus_hip.h is the same loop with the sampling on device logits and no
+ * EOS stop.)  Replaces reference qorus.h:302-320 / src/main.c:994-1131. */
+q_error_code q_generate(q_generation_state* Q_RESTRICT state);
+
+/* ---- BPE tokenizer (host; reference include/qorus.h:224-273,
+ *      src/tokenizer/bpe.c) ---- */
+
+/* Load a 'QTKR' v1 tokenizer file (32-byte header, length-prefixed vocab
+ * strings, (id1, id2, merged) rules).  Same validation order and codes as
+ * the reference.  Replaces reference qorus.h:226-230 / bpe.c:263-... */
+q_error_code q_tokenizer_load(q_tokenizer* Q_RESTRICT tok, const char* tokenizer_path);
+
+/* Text -> ids: one token per byte, the merge rules applied greedily in file
+ * order until nothing changes, BOS/EOS on request; Q_ERR_ARENA_OOM when the
+ * result exceeds max_tokens.  Replaces reference qorus.h:232-250 /
+ * bpe.c:692-808. */
+q_error_code q_tokenizer_encode(q_tokenizer* Q_RESTRICT tok, const char* Q_RESTRICT text,
+                                uint32_t* Q_RESTRICT tokens_out, uint32_t* Q_RESTRICT num_tokens_out,
+                                uint32_t max_tokens, bool add_bos, bool add_eos);
+
+/* Ids -> text (special and out-of-vocabulary ids skipped; Q_ERR_ARENA_OOM
+ * and a truncated text when the buffer is short).  Replaces reference
+ * qorus.h:252-266 / bpe.c:811-866. */
+q_error_code q_tokenizer_decode(q_tokenizer* Q_RESTRICT tok, const uint32_t* Q_RESTRICT tokens,
+                                uint32_t num_tokens, char* Q_RESTRICT text_out, size_t text_buf_size);
+
+/* Free what q_tokenizer_load allocated and zero the struct.
+ * Replaces reference qorus.h:268-273 / bpe.c:869-887. */
+void q_tokenizer_free(q_tokenizer* Q_RESTRICT tok);
 
 #ifdef __cplusplus
 }

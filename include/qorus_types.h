@@ -72,8 +72,9 @@ typedef enum {
     Q_Q4_0 = 2
 } q_dtype;
 
-/* BPE tokenizer state.  The tokenizer itself is outside the MI355X build;
- * the type is kept because q_generation_state embeds a pointer to it. */
+/* BPE tokenizer state (q_tokenizer_load / encode / decode / free).
+ * merge_hash_table is the library's own lookup table (opaque; NULL for a
+ * tokenizer assembled by hand, whose rules then use merges[i].merged_id). */
 typedef struct {
     uint32_t token_id1;
     uint32_t token_id2;

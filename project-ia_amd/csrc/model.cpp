@@ -22,6 +22,7 @@
 #include <cmath>
 #include <cstdint>
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -796,6 +797,50 @@ q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restr
     QH_TRY(hipStreamSynchronize(p->stream));
     std::memcpy(logits, p->pinned_logits, (size_t)model->config.vocab_size * 4);
     return Q_OK;
+}
+
+// Reference src/main.c:994-1131, validation in its order: NULL state, ctx,
+// model, tokenizer, prompt_tokens or generated_tokens -> INVALID_ARG; no
+// prompt tokens or max_tokens 0 -> INVALID_SIZE; temperature negative, NaN or
+// infinite -> INVALID_ARG; tokenizer not initialized, no arena or no KV
+// cache -> INVALID_ARG; a prompt longer than max_seq_len -> INVALID_SIZE.
+// Then: the prompt at position 0, and per step a draw from the last logits
+// (q_sample_token with the context's arena; the logits in 64-byte-aligned
+// host memory, as the reference allocates them), a stop at EOS or a full
+// context, the token forwarded at the next position; the arena is reset
+// before each forward.
+q_error_code q_generate(q_generation_state* __restrict__ st) {
+    if (!st || !st->ctx || !st->model || !st->tokenizer || !st->prompt_tokens || !st->generated_tokens)
+        return Q_ERR_INVALID_ARG;
+    if (st->num_prompt_tokens == 0 || st->max_tokens == 0) return Q_ERR_INVALID_SIZE;
+    if (!(st->temperature >= 0.0f) || !std::isfinite(st->temperature)) return Q_ERR_INVALID_ARG;
+    if (!st->tokenizer->initialized) return Q_ERR_INVALID_ARG;
+    if (!st->ctx->scratch_buffer || !st->ctx->kv_buffer) return Q_ERR_INVALID_ARG;
+    const uint32_t V = st->model->config.vocab_size, max_seq = st->model->config.max_seq_len;
+    if (st->num_prompt_tokens > max_seq) return Q_ERR_INVALID_SIZE;
+    st->num_generated_tokens = 0;
+    st->current_pos = 0;
+    q_arena_reset(st->ctx);
+    float* logits = static_cast<float*>(std::aligned_alloc(Q_ALIGN, Q_ALIGN_SIZE((size_t)V * sizeof(float))));
+    if (!logits) return Q_ERR_ALLOC_FAILED;
+    q_error_code rc = llama_forward(st->model, st->ctx, st->prompt_tokens, st->num_prompt_tokens, 0, logits);
+    if (rc == Q_OK) st->current_pos = st->num_prompt_tokens;
+    while (rc == Q_OK && st->num_generated_tokens < st->max_tokens && st->current_pos < max_seq) {
+        uint32_t tok = 0;
+        rc = q_sample_token(logits, V, st->temperature, st->top_k, st->top_p, &tok, st->ctx);
+        if (rc != Q_OK) break;
+        if (tok >= V) {
+            rc = Q_ERR_INVALID_ARG;
+            break;
+        }
+        st->generated_tokens[st->num_generated_tokens++] = tok;
+        if (tok == st->tokenizer->eos_token_id) break;
+        q_arena_reset(st->ctx);
+        rc = llama_forward(st->model, st->ctx, &tok, 1, st->current_pos, logits);
+        if (rc == Q_OK) ++st->current_pos;
+    }
+    std::free(logits);
+    return rc;
 }
 
 // Greedy generation on the device: n_steps decode steps from (token, pos),

@@ -23,5 +23,6 @@ from ._lib import (  # noqa: F401
     ERR,
 )
 from .model_file import write_qorus_v3, model_layout, QorusHeader  # noqa: F401
-from .model import Model, QContext, QLlamaModel  # noqa: F401
+from .model import Model, QContext, QLlamaModel, QGenerationState  # noqa: F401
+from .tokenizer import Tokenizer, QTokenizer, write_tokenizer, byte_level_vocab  # noqa: F401
 from . import synthetic  # noqa: F401

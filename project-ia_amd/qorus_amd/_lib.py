@@ -156,6 +156,12 @@ def lib():
     _sig(L, "q_matmul_f32_avx2", i32, vp, vp, vp, vp)
     _sig(L, "q_mul_f32_avx2", i32, vp, vp, vp)
     _sig(L, "q_causal_mask_f32_avx2", i32, vp, f32)
+    # tokenizer and generation loop (host)
+    _sig(L, "q_tokenizer_load", i32, vp, C.c_char_p)
+    _sig(L, "q_tokenizer_encode", i32, vp, C.c_char_p, vp, vp, u32, C.c_bool, C.c_bool)
+    _sig(L, "q_tokenizer_decode", i32, vp, vp, u32, vp, C.c_size_t)
+    _sig(L, "q_tokenizer_free", None, vp)
+    _sig(L, "q_generate", i32, vp)
     _sig(L, "qh_causal_mask_f32", i32, vp, u32, u32, f32, vp)
     _sig(L, "qh_rmsnorm_f32", i32, vp, vp, vp, u32, f32, vp)
     _sig(L, "qh_rope_f32", i32, vp, vp, vp, vp, u32, u32, vp)

@@ -36,6 +36,15 @@ class QLlamaModel(C.Structure):
 assert C.sizeof(QContext) == 72 and C.sizeof(QLlamaModel) == 112
 
 
+class QGenerationState(C.Structure):
+    """q_generation_state (include/qorus_types.h)."""
+    _fields_ = [("ctx", C.c_void_p), ("model", C.c_void_p), ("tokenizer", C.c_void_p),
+                ("prompt_tokens", C.c_void_p), ("num_prompt_tokens", C.c_uint32),
+                ("generated_tokens", C.c_void_p), ("num_generated_tokens", C.c_uint32),
+                ("max_tokens", C.c_uint32), ("temperature", C.c_float), ("top_k", C.c_uint32),
+                ("top_p", C.c_float), ("current_pos", C.c_uint32)]
+
+
 class Model:
     """A loaded v3 model with an HBM KV cache sized for its max_seq_len."""
 
@@ -92,6 +101,17 @@ class Model:
                                               top_k, top_p, out.ctypes.data, C.byref(ms)),
               "qh_llama_generate_sampled")
         return out, float(ms.value)
+
+    def q_generate(self, tokenizer, prompt, max_tokens: int, temperature: float = 0.0, top_k: int = 0,
+                   top_p: float = 0.0):
+        """q_generate from position 0: returns (generated token ids,
+        current_pos); raises QorusError on a failing code."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        st = QGenerationState(C.addressof(self.ctx), C.addressof(self.model), C.addressof(tokenizer.t),
+                              p.ctypes.data, p.size, out.ctypes.data, 0, max_tokens, temperature, top_k, top_p, 0)
+        check(lib().q_generate(C.byref(st)), "q_generate")
+        return out[:st.num_generated_tokens].tolist(), st.current_pos
 
     def close(self):
         if not self._closed:

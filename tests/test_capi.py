@@ -50,8 +50,9 @@ def test_library_exports_every_declared_symbol():
 def declared_prototypes():
     """{name: (return kind, [parameter kinds])} from include/*.h, each type
     reduced to its ABI class: "ptr" (any pointer or handle), "i32", "u32",
-    "u64", "f32", "void"."""
-    scalar = {"int": "i32", "uint32_t": "u32", "uint64_t": "u64", "size_t": "u64", "float": "f32", "void": "void"}
+    "u64", "f32", "bool", "void"."""
+    scalar = {"int": "i32", "uint32_t": "u32", "uint64_t": "u64", "size_t": "u64", "float": "f32", "void": "void",
+              "bool": "bool"}
     types = (REPO / "include" / "qorus_types.h").read_text()
     for enum in re.findall(r"typedef\s+enum\s*\{[^}]*\}\s*(\w+)\s*;", types):
         scalar[enum] = "i32"
@@ -86,6 +87,8 @@ def ctypes_kind(t):
         return "ptr"
     if t is C.c_float:
         return "f32"
+    if t is C.c_bool:
+        return "bool"
     if t in (C.c_int, C.c_int32):
         return "i32"
     if t in (C.c_uint32, C.c_uint):
