@@ -633,37 +633,59 @@ def run_cpu_prefill(rows=12):
 # HBM traffic of the dominant kernel (rocprofv3 --pmc passes)
 # ---------------------------------------------------------------------------
 COPY_BYTES = 256 << 20
-TRAFFIC_LAUNCHES = 24
+TRAFFIC_LAUNCHES = 12
+
+
+TRAFFIC_SHAPES = [("qkv", "h", ["wq", "wk", "wv"]), ("wo", "o", ["wo"]), ("gate_up", "h2", ["w_gate", "w_up"]),
+                  ("down", "m", ["w_down"]), ("lm_head", "h", ["lm"])]
+LM_VOCAB = 128256
+
+
+def traffic_alg_bytes(name):
+    if name == "lm_head":
+        return alg_bytes(LM_VOCAB, DIM)
+    mats = dict((n, m) for n, _, m in TRAFFIC_SHAPES)[name]
+    return sum(alg_bytes(M, N) for k, M, N in SHAPES if k in mats)
 
 
 def run_traffic():
-    """Workload of the counter passes: TRAFFIC_LAUNCHES fused W_gate|W_up
-    GEMV launches (rotating LAYERS distinct weight sets) and 4 device copies
-    of COPY_BYTES, whose counter readings calibrate the KiB-per-dispatch
-    scale.  Run it under `rocprofv3 --pmc FETCH_SIZE` and, separately,
-    `--pmc WRITE_SIZE`; then --summarize-traffic."""
+    """Workload of the counter passes: for each GEMV launch shape of the
+    decode step (Q|K|V, Wo, W_gate|W_up, W_down, each from its fp32 input)
+    and the config-3 LM head (128256 x 4096), TRAFFIC_LAUNCHES launches in
+    a block (rotating the weight sets), then 4 device copies of COPY_BYTES
+    whose counter readings calibrate the KiB-per-dispatch scale.  Run it
+    under `rocprofv3 --pmc FETCH_SIZE` and, separately, `--pmc WRITE_SIZE`;
+    then --summarize-traffic."""
     import qorus_amd as qa
     from qorus_amd import synthetic as syn
     lib = qa.lib()
     if not qa.gpu_available():
         raise SystemExit("bench.py: no usable GPU")
     layers = [LayerSet(qa, gen_layer(1000 + l)) for l in range(LAYERS)]
-    x = qa.DeviceBuffer.from_numpy(syn.gen_f32(DIM, syn.rng_for(77)))
-    ws = qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(DIM))
-    outs = [qa.DeviceBuffer(HID * 4) for _ in range(2)]
+    rng = syn.rng_for(91)
+    lm = [qa.DeviceBuffer.from_numpy(syn.gen_q4(LM_VOCAB, DIM, rng)) for _ in range(2)]
+    lm_t = [qa.q4_tensor(b.ptr, LM_VOCAB, DIM) for b in lm]
+    xin = {k: qa.DeviceBuffer.from_numpy(syn.gen_f32(n, syn.rng_for(77))) for k, n in
+           (("h", DIM), ("o", DIM), ("h2", DIM), ("m", HID))}
+    ws = {k: qa.DeviceBuffer(lib.qh_gemv_workspace_bytes(n)) for k, n in
+          (("h", DIM), ("o", DIM), ("h2", DIM), ("m", HID))}
+    outs = {k: qa.DeviceBuffer(M * 4) for k, M, _ in SHAPES}
+    outs["lm"] = qa.DeviceBuffer(LM_VOCAB * 4)
     src, dst = qa.DeviceBuffer(COPY_BYTES), qa.DeviceBuffer(COPY_BYTES)
     stream = qa.Stream()
     s = stream.handle
-    ys = ptr_array([o.ptr for o in outs])
-    for i in range(TRAFFIC_LAUNCHES):
-        L = layers[i % LAYERS]
-        Ws = ptr_array([L.t["w_gate"].addr, L.t["w_up"].addr])
-        qa.check(lib.qh_gemv_q4_f32_multi(Ws, None, ys, 2, x.ptr, ws.ptr, s))
-    stream.sync()
+    for name, xk, mats in TRAFFIC_SHAPES:
+        for i in range(TRAFFIC_LAUNCHES):
+            L = layers[i % LAYERS]
+            Ws = ptr_array([(lm_t[i % 2] if m == "lm" else L.t[m]).addr for m in mats])
+            ys = ptr_array([outs[m].ptr for m in mats])
+            qa.check(lib.qh_gemv_q4_f32_multi(Ws, None, ys, len(mats), xin[xk].ptr, ws[xk].ptr, s))
+        stream.sync()
     for _ in range(4):
         qa.check(lib.qh_memcpy_dtod(dst.ptr, src.ptr, COPY_BYTES, s))
     stream.sync()
-    print(json.dumps({"traffic_workload": "gate_up", "launches": TRAFFIC_LAUNCHES, "copy_bytes": COPY_BYTES}))
+    print(json.dumps({"traffic_workload": [n for n, _, _ in TRAFFIC_SHAPES], "launches": TRAFFIC_LAUNCHES,
+                      "copy_bytes": COPY_BYTES}))
 
 
 def _counter_rows(d):
@@ -677,38 +699,48 @@ def _counter_rows(d):
 
 
 def summarize_traffic(fetch_dir, write_dir, cmd):
-    """profiles/gemv_gate_up_traffic.json from the two counter passes.
-    Each counter's KiB-per-dispatch reading is scaled by copy_bytes / (what
-    the same counter reads for the device copy), so the figure is in bytes
-    of the copy's own accounting."""
-    out = {}
-    for name, d, copy_side in (("FETCH_SIZE", fetch_dir, "read"), ("WRITE_SIZE", write_dir, "write")):
-        rows = [r for r in _counter_rows(d) if r.get("Counter_Name") == name]
-        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv" in r["Kernel_Name"]]
+    """profiles/gemv_traffic.json from the two counter passes.  The GEMV
+    dispatches, in dispatch order, are the blocks of TRAFFIC_SHAPES; each
+    counter's KiB-per-dispatch reading (median of a block, its first two
+    launches left out) is scaled by copy_bytes / (what the same counter
+    reads for the device copy), so the figure is in bytes of the copy's own
+    accounting."""
+    per = {n: {} for n, _, _ in TRAFFIC_SHAPES}
+    cal = {}
+    for cname, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = [r for r in _counter_rows(d) if r.get("Counter_Name") == cname]
+        gemv = sorted((r for r in rows if "k_gemv" in r["Kernel_Name"]), key=lambda r: int(r["Dispatch_Id"]))
         copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
         gmax = max((int(r["Grid_Size"]) for r in copies), default=0)
         copy = [float(r["Counter_Value"]) for r in copies if int(r["Grid_Size"]) == gmax]
-        if not gemv or not copy:
-            raise SystemExit(f"{name}: no gemv ({len(gemv)}) or copy ({len(copy)}) dispatches")
-        g = float(np.median(gemv[2:] if len(gemv) > 4 else gemv))
+        if len(gemv) != TRAFFIC_LAUNCHES * len(TRAFFIC_SHAPES) or not copy:
+            raise SystemExit(f"{cname}: {len(gemv)} gemv dispatches, {len(copy)} copies")
         c = float(np.median(copy))
         factor = COPY_BYTES / (c * 1024.0)
-        out[name] = {"gemv_kib_per_dispatch": g, "copy_kib_per_dispatch": c, "copy_bytes": COPY_BYTES,
-                     "scale": factor, "gemv_bytes_per_dispatch": g * 1024.0 * factor,
-                     "n_gemv": len(gemv), "n_copy": len(copy)}
-    traffic = out["FETCH_SIZE"]["gemv_bytes_per_dispatch"] + out["WRITE_SIZE"]["gemv_bytes_per_dispatch"]
+        cal[cname] = {"copy_kib_per_dispatch": c, "copy_bytes": COPY_BYTES, "scale": factor}
+        for i, (name, _, _) in enumerate(TRAFFIC_SHAPES):
+            block = [float(r["Counter_Value"]) for r in gemv[i * TRAFFIC_LAUNCHES:(i + 1) * TRAFFIC_LAUNCHES]]
+            g = float(np.median(block[2:]))
+            per[name][cname] = {"kib_per_dispatch": g, "bytes_per_dispatch": g * 1024.0 * factor}
+    shapes = {}
+    for name, _, _ in TRAFFIC_SHAPES:
+        t = per[name]["FETCH_SIZE"]["bytes_per_dispatch"] + per[name]["WRITE_SIZE"]["bytes_per_dispatch"]
+        alg = traffic_alg_bytes(name)
+        shapes[name] = {"alg_bytes_per_launch": alg, "traffic_bytes_per_launch": round(t),
+                        "traffic_over_alg": round(t / alg, 4), "counters": per[name]}
     res = {"kernel": "k_gemv_p fused W_gate|W_up 28672x4096 (config 2)", "alg_bytes_per_launch": GATE_UP_BYTES,
-           "traffic_bytes_per_launch": round(traffic), "traffic_over_alg": round(traffic / GATE_UP_BYTES, 4),
-           "counters": out, "command": cmd}
-    p = REPO / "profiles" / "gemv_gate_up_traffic.json"
+           "traffic_bytes_per_launch": shapes["gate_up"]["traffic_bytes_per_launch"],
+           "traffic_over_alg": shapes["gate_up"]["traffic_over_alg"], "shapes": shapes, "calibration": cal,
+           "command": cmd}
+    p = REPO / "profiles" / "gemv_traffic.json"
     p.write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res))
 
 
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 --pmc summary (profiles/gemv_gate_up_traffic.json), or None."""
-    p = REPO / "profiles" / "gemv_gate_up_traffic.json"
+    rocprofv3 --pmc summary (profiles/gemv_traffic.json), or None."""
+    p = REPO / "profiles" / "gemv_traffic.json"
     try:
         return json.loads(p.read_text()).get("traffic_bytes_per_launch")
     except (OSError, ValueError):
@@ -769,7 +801,7 @@ def main():
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="write profiles/gemv_gate_up_traffic.json from two --pmc output dirs")
+                    help="write profiles/gemv_traffic.json from two --pmc output dirs")
     ap.add_argument("--traffic-cmd", default="", help="command line recorded with the summary")
     args = ap.parse_args()
     if args.summarize_traffic:
