@@ -126,7 +126,8 @@ q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const*
  * non-finite value yields NaN outputs.
  * Validation, per matrix and in this order: W, X or Y NULL -> INVALID_ARG;
  * X not 16-byte or Y not 4-byte aligned -> MISALIGNED; M == 0, N == 0,
- * N % 32, N differing between the matrices or T == 0 -> INVALID_SIZE;
+ * N % 32, N > 32768, N differing between the matrices or T == 0 ->
+ * INVALID_SIZE;
  * type != Q4_0 -> INVALID_DTYPE; N/32 > UINT32_MAX/M or M*N/32*20 >= 2^31
  * -> OVERFLOW; nb[0] != N/32*20 or W->data NULL -> INVALID_ARG; W->data
  * not 4-byte aligned -> MISALIGNED; Y overlapping X -> ALIASING; then

@@ -238,7 +238,7 @@ q_error_code qh_gemm_q4_f32_multi(const q_tensor* const* Ws, float* const* Ys, u
         if (!W || !Ys || !Ys[i] || !X) return Q_ERR_INVALID_ARG;
         if (!aligned(X, 16) || !aligned(Ys[i], 4)) return Q_ERR_MISALIGNED;
         const uint32_t Mi = W->ne[0], N = W->ne[1];
-        if (Mi == 0 || N == 0 || N % 32 != 0 || N != Ws[0]->ne[1] || T == 0) return Q_ERR_INVALID_SIZE;
+        if (Mi == 0 || N == 0 || N % 32 != 0 || N > 32768 || N != Ws[0]->ne[1] || T == 0) return Q_ERR_INVALID_SIZE;
         if (W->type != Q_Q4_0) return Q_ERR_INVALID_DTYPE;
         if (N / 32 > UINT32_MAX / Mi || (uint64_t)Mi * (N / 32) * 20u >= (1ull << 31)) return Q_ERR_OVERFLOW;
         if (W->nb[0] != (size_t)(N / 32) * sizeof(q_block_q4_0)) return Q_ERR_INVALID_ARG;

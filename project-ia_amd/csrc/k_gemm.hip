@@ -76,43 +76,82 @@ struct GemmXIn {
     float eps;
 };
 
+constexpr uint32_t kXpMaxGroups = 16;  // 8-element groups per thread: rows of up to 32768 elements
+
+template <uint32_t kXpGroups>
 __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T, uint32_t N, uint32_t N_pad,
                                                     _Float16* __restrict__ xh, _Float16* __restrict__ xl,
                                                     float2* __restrict__ meta) {
-    __shared__ float red_m[4];
+    __shared__ float red[4];
     __shared__ int red_f[4];
     const uint32_t t = blockIdx.x;
     const bool valid = t < T;  // uniform over the workgroup
-    const float* xr = in.x + (size_t)t * N;
-    const float* ur = in.u ? in.u + (size_t)t * N : nullptr;
-    float r = 1.0f;
-    if (valid && in.norm_w) r = rms_scale<256>(xr, N, in.eps, red_m);
-    auto value = [&](uint32_t k) -> float {
-        const float v = xr[k];
-        if (ur) return silu_approx(v) * ur[k];
-        if (in.norm_w) return (v * r) * in.norm_w[k];
-        return v;
-    };
-    float m = 0.0f;
-    int nf = 0;
-    if (valid) {
-        for (uint32_t i = threadIdx.x; i < N; i += 256) {
-            const float v = value(i);
-            nf |= !__builtin_isfinite(v);
-            m = fmaxf(m, fabsf(v));
+    const uint32_t ng = N_pad / 8, nv = valid ? N / 8 : 0u;  // groups of the padded row / holding data
+    const float4* x4 = reinterpret_cast<const float4*>(in.x + (size_t)t * N);
+    const float4* u4 = in.u ? reinterpret_cast<const float4*>(in.u + (size_t)t * N) : nullptr;
+    // The thread's groups g = tid + 256*i, read once (two 16-byte loads each).
+    float v[kXpGroups][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kXpGroups; ++i) {
+        const uint32_t g = threadIdx.x + 256u * i;
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (g < nv) {
+            a = x4[2 * g];
+            b = x4[2 * g + 1];
+        }
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+        if (in.norm_w) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = ss + v[i][e] * v[i][e];
+        }
+        if (u4 && g < nv) {
+            const float4 c = u4[2 * g], d = u4[2 * g + 1];
+            const float uu[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[i][e] = silu_approx(v[i][e]) * uu[e];
         }
     }
+    if (in.norm_w) {
+        // r = newton(rsq(sum/N + eps)), the RMSNorm factor of reference
+        // rmsnorm.c:62-71 (the sum in this kernel's fixed order)
+        const float sum = block_sum<256>(ss, red);
+        const float av = sum / (float)N + in.eps;
+        const float r0 = __builtin_amdgcn_rsqf(av);
+        const float r = (r0 * (3.0f - av * (r0 * r0))) * 0.5f;
+        const float4* w4 = reinterpret_cast<const float4*>(in.norm_w);
+#pragma unroll
+        for (uint32_t i = 0; i < kXpGroups; ++i) {
+            const uint32_t g = threadIdx.x + 256u * i;
+            if (g < nv) {
+                const float4 c = w4[2 * g], d = w4[2 * g + 1];
+                const float ww[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[i][e] = (v[i][e] * r) * ww[e];
+            }
+        }
+    }
+    float m = 0.0f;
+    int nf = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kXpGroups; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            nf |= !__builtin_isfinite(v[i][e]);
+            m = fmaxf(m, fabsf(v[i][e]));
+        }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         m = fmaxf(m, __shfl_xor(m, off));
         nf |= __shfl_xor(nf, off);
     }
     if ((threadIdx.x & 63) == 0) {
-        red_m[threadIdx.x >> 6] = m;
+        red[threadIdx.x >> 6] = m;
         red_f[threadIdx.x >> 6] = nf;
     }
     __syncthreads();
-    m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     nf = red_f[0] | red_f[1] | red_f[2] | red_f[3];
     int e = 0;
     if (!nf && m > 0.0f) {
@@ -122,18 +161,21 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T
     }
     _Float16* hr = xh + (size_t)t * N_pad;
     _Float16* lr = xl + (size_t)t * N_pad;
-    for (uint32_t g = threadIdx.x; g < N_pad / 8; g += 256) {
-        h8v hv, lv;
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const uint32_t k = g * 8 + (uint32_t)perm8(p);
-            const float v = (valid && !nf && k < N) ? ldexpf(value(k), e) : 0.0f;
-            const _Float16 h = (_Float16)v;
-            hv[p] = h;
-            lv[p] = (_Float16)((v - (float)h) * 2048.0f);  // exact difference, exact scaling
+    for (uint32_t i = 0; i < kXpGroups; ++i) {
+        const uint32_t g = threadIdx.x + 256u * i;
+        if (g < ng) {
+            h8v hv, lv;
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const float w = nf ? 0.0f : ldexpf(v[i][perm8(p)], e);
+                const _Float16 h = (_Float16)w;
+                hv[p] = h;
+                lv[p] = (_Float16)((w - (float)h) * 2048.0f);  // exact difference, exact scaling
+            }
+            *reinterpret_cast<h8v*>(hr + g * 8) = hv;
+            *reinterpret_cast<h8v*>(lr + g * 8) = lv;
         }
-        *reinterpret_cast<h8v*>(hr + g * 8) = hv;
-        *reinterpret_cast<h8v*>(lr + g * 8) = lv;
     }
     if (threadIdx.x == 0) meta[t] = make_float2(ldexpf(1.0f, -e), nf ? 1.0f : 0.0f);
 }
@@ -418,6 +460,7 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     const uint32_t N = in.N, T = in.T;
     const int nseg = sg.n;
     if (nseg < 1 || nseg > kGemmMaxSeg || T == 0 || N == 0 || N % 32 != 0 || !in.x) return hipErrorInvalidValue;
+    if (gemm_npad(N) > 8u * 256u * kXpMaxGroups) return hipErrorInvalidValue;  // the row conversion's register tile
     if (in.norm_w && in.u) return hipErrorInvalidValue;
     const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
     uint8_t* p = static_cast<uint8_t*>(ws);
@@ -452,7 +495,11 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     // The XCD-aware order needs the token-tile count to divide the 8 XCDs.
     a.xcd_map = (8u % a.n_tt == 0) ? 1u : 0u;
     const GemmXIn xin{in.x, in.u, in.norm_w, in.eps};
-    hipLaunchKernelGGL(k_gemm_xprep, dim3(tp), dim3(256), 0, s, xin, T, N, np, const_cast<_Float16*>(a.xh),
+    // the smallest register tile holding the row: groups of 8 per thread
+    const uint32_t per = (np / 8 + 255) / 256;
+    auto xprep = per <= 2 ? k_gemm_xprep<2> : per <= 4 ? k_gemm_xprep<4> : per <= 8 ? k_gemm_xprep<8>
+                                                                             : k_gemm_xprep<16>;
+    hipLaunchKernelGGL(xprep, dim3(tp), dim3(256), 0, s, xin, T, N, np, const_cast<_Float16*>(a.xh),
                        const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -84,13 +84,15 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 // Causal prefill attention on v_mfma_f32_16x16x4_f32.
 //
 // Workgroup: 16 queries (a query tile) x the G query heads of one KV head,
-// one wave per head; the G waves share the key/value rows, staged in LDS 64
-// keys at a time.  Per query (as in the decode step): s_j = (q . k_j) *
-// scale for j <= P (its position), m = max_j s_j, e_j = exp_approx(s_j - m)
-// for j < (P+1) & ~7 and expf above (all expf when P+1 < 8), o = sum_j e_j v_j
-// times 1/sum_j e_j (divided by the sum when P+1 < 8).  The polynomial exp
-// is not multiplicative, so the max is found in a first pass over the keys
-// and the scores are recomputed (bit-identically) in the second.
+// two waves per head, each taking half of every staged 64-key block (so a
+// tile's serial chain is half its keys); the 2G waves share the key/value
+// rows, staged in LDS 64 keys at a time.  Per query (as in the decode step):
+// s_j = (q . k_j) * scale for j <= P (its position), m = max_j s_j,
+// e_j = exp_approx(s_j - m) for j < (P+1) & ~7 and expf above (all expf when
+// P+1 < 8), o = sum_j e_j v_j times 1/sum_j e_j (divided by the sum when
+// P+1 < 8).  The polynomial exp is not multiplicative, so the max is found in
+// a first pass over the keys and the scores are recomputed (bit-identically)
+// in the second; the two halves' maxima, sums and P.V partials meet in LDS.
 //
 // Fragment layouts (16x16x4: lane l feeds A[l%16][l/16] and B[l/16][l%16];
 // D[4*(l/16)+r][l%16] lands in register r of lane l):
@@ -110,19 +112,21 @@ constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
 
 template <uint32_t G>
-__global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a) {
-    constexpr uint32_t NT = 64 * G;
+__global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs a) {
+    constexpr uint32_t NT = 128 * G;
     constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
     static_assert(kLoads * NT == kAttnKS * (kPHd / 4), "stage/thread mismatch");
-    __shared__ __attribute__((aligned(16))) float lk[kAttnKS][kAttnRS];
-    __shared__ __attribute__((aligned(16))) float lv[kAttnKS][kAttnRS];
+    static_assert(G * 64 * 32 <= 2 * kAttnKS * kAttnRS, "the P.V exchange reuses the staging space");
+    __shared__ __attribute__((aligned(16))) float lkv[2][kAttnKS][kAttnRS];  // [0] K rows, [1] V rows
+    __shared__ float xmax[2][G][16], xsum[G][16];
 
     const uint32_t n_qt = (a.T + 15) / 16;
     const uint32_t qt = n_qt - 1 - blockIdx.x;  // the longest rows first
     const uint32_t kvh = blockIdx.y;
     const uint32_t t0 = qt * 16;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t h = kvh * G + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t hw = wave % G, half = wave / G;  // head within the group, half of each block
+    const uint32_t h = kvh * G + hw;
     const uint32_t li = lane & 15, lg = lane >> 4;
     const uint32_t t_last = min(t0 + 15u, a.T - 1u);
     const uint32_t n_keys = a.pos0 + t_last + 1u;  // keys of the tile's last query
@@ -168,8 +172,8 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
-            *reinterpret_cast<float4*>(&lk[r][4 * c]) = kr[u];
-            if (with_v) *reinterpret_cast<float4*>(&lv[r][4 * c]) = vr[u];
+            *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) = kr[u];
+            if (with_v) *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) = vr[u];
         }
     };
 
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
     // applied by the caller): two accumulation chains, then their sum.
     auto scores = [&](uint32_t sub) -> f4v {
         f4v d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const float* kr = &lk[sub * 16 + li][32 * lg];
+        const float* kr = &lkv[0][sub * 16 + li][32 * lg];
 #pragma unroll
         for (int c = 0; c < 8; c += 2) {
             const float4 k0 = *reinterpret_cast<const float4*>(kr + 4 * c);
@@ -194,14 +198,15 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
         return d0 + d1;
     };
 
-    // ---- pass 1: row max ----
+    // ---- pass 1: row max (this half's keys, then both halves) ----
     float mx = -INFINITY;
     for (uint32_t st = 0; st < n_stages; ++st) {
         __syncthreads();  // the previous stage's reads are done
         stage(st, false);
         __syncthreads();
 #pragma unroll
-        for (uint32_t sub = 0; sub < kAttnKS / 16; ++sub) {
+        for (uint32_t s2 = 0; s2 < 2; ++s2) {
+            const uint32_t sub = 2 * half + s2;
             const uint32_t jb = st * kAttnKS + sub * 16;
             if (jb >= n_keys) break;
             const f4v d = scores(sub);
@@ -215,8 +220,11 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (lane < 16) xmax[half][hw][lane] = mx;
+    __syncthreads();
+    mx = fmaxf(xmax[0][hw][li], xmax[1][hw][li]);
 
-    // ---- pass 2: e_j, their sum and P.V ----
+    // ---- pass 2: e_j, their sum and P.V over this half's keys ----
     f4v acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -226,7 +234,8 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
         stage(st, true);
         __syncthreads();
 #pragma unroll
-        for (uint32_t sub = 0; sub < kAttnKS / 16; ++sub) {
+        for (uint32_t s2 = 0; s2 < 2; ++s2) {
+            const uint32_t sub = 2 * half + s2;
             const uint32_t jb = st * kAttnKS + sub * 16;
             if (jb >= n_keys) break;
             const f4v d = scores(sub);
@@ -242,7 +251,7 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
             }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const float* vr = &lv[sub * 16 + 4 * lg + kk][0];
+                const float* vr = &lkv[1][sub * 16 + 4 * lg + kk][0];
                 const float4 v0 = *reinterpret_cast<const float4*>(vr + 4 * li);
                 const float4 v1 = *reinterpret_cast<const float4*>(vr + 64 + 4 * li);
                 acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.x, acc[0], 0, 0, 0);
@@ -258,6 +267,21 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
+
+    // ---- the second half's partials join the first's through LDS (the
+    // staging space, free after this barrier) ----
+    __syncthreads();
+    float* xo = &lkv[0][0][0] + (size_t)(hw * 64 + lane) * 32;
+    if (half == 1) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) *reinterpret_cast<f4v*>(xo + 4 * t) = acc[t];
+        if (lane < 16) xsum[hw][lane] = sum;
+    }
+    __syncthreads();
+    if (half == 1) return;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] += *reinterpret_cast<const f4v*>(xo + 4 * t);
+    sum += xsum[hw][li];
 
     // ---- output: register r of lane l is query 4*(l/16) + r ----
 #pragma unroll
@@ -281,7 +305,7 @@ __global__ __launch_bounds__(64 * G) void k_prefill_attn(const PrefillAttnArgs a
 template <uint32_t G>
 static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
     const uint32_t n_qt = (a.T + 15) / 16;
-    hipLaunchKernelGGL(k_prefill_attn<G>, dim3(n_qt, a.n_kv), dim3(64 * G), 0, s, a);
+    hipLaunchKernelGGL(k_prefill_attn<G>, dim3(n_qt, a.n_kv), dim3(128 * G), 0, s, a);
     return hipGetLastError();
 }
 
