@@ -11,14 +11,12 @@
 //    s in fp32 (inner += s * D), so W enters the matrix core exactly.
 //  * X: each token row is scaled by a power of two 2^e (max |x| in
 //    [2^14, 2^15)) and split into two fp16 parts: hi = rn(x') and
-//    lo = rn((x' - hi) * 2^11) (the subtraction and the power-of-two
-//    scaling are exact in fp32).  lo is kept 2^11 above its natural size, so
-//    it stays an fp16 normal wherever hi is (every element within 2^29 of
-//    the row maximum: activation outliers do not cost the other elements
-//    their low bits), and its MFMA takes the weight operand times 2^-11
-//    (exact in fp16).  The two parts hold 22 significant bits of every such
-//    element.  Two MFMAs per block (hi, lo) accumulate into the same D; the
-//    products (q-8)*hi and (q-8)*2^-11*lo are exact.
+//    lo = rn(x' - hi) (the subtraction is exact in fp32).  The two parts hold
+//    22 significant bits of every element whose lo is an fp16 normal
+//    (|x'| >= 2^-3: within 2^17 of the row maximum); smaller elements keep
+//    hi's 11 bits plus what the subnormal lo holds (steps of 2^-24).  Two
+//    MFMAs per block (hi, lo) against the same weight operand accumulate
+//    into one D; the products (q-8)*hi and (q-8)*lo are exact.
 //  * Accumulation: a block's D feeds an inner fp32 sum over kInner blocks,
 //    which is added to an outer sum (two-level summation): max error
 //    relative to sum_k |W x| stays at or below the reference AVX2 order's
@@ -171,7 +169,7 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T
                 const float w = nf ? 0.0f : ldexpf(v[i][perm8(p)], e);
                 const _Float16 h = (_Float16)w;
                 hv[p] = h;
-                lv[p] = (_Float16)((w - (float)h) * 2048.0f);  // exact difference, exact scaling
+                lv[p] = (_Float16)(w - (float)h);  // the exact difference, rounded
             }
             *reinterpret_cast<h8v*>(hr + g * 8) = hv;
             *reinterpret_cast<h8v*>(lr + g * 8) = lv;
@@ -200,7 +198,7 @@ struct GemmArgs {
     uint32_t blk_per_split;
     uint32_t xcd_map;     // 1: XCD-aware tile order
     const _Float16* xh;
-    const _Float16* xl;   // the low part, times 2^11
+    const _Float16* xl;   // the low part
     const float2* meta;
     float* part;          // [split][T][M_total-slot] partials (split > 1)
     uint32_t part_ld;     // partial row length (sum of segment M)
@@ -353,13 +351,12 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         if (step + 1 < nsteps) load_step(step + 1);
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
-            h8v B[4], Bs[4];  // Bs = B * 2^-11 (exact), the operand of lo
+            h8v B[4];
             float s[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 64 * wm + 16 * i + lr;
                 B[i] = unpack8(lw[buf][r][kb][lq]);
-                Bs[i] = B[i] * (_Float16)0.00048828125f;
                 s[i] = ls[buf][r][kb];
             }
             // One token subtile at a time: its hi and lo parts, then the 4
@@ -372,7 +369,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Bs[i], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B[i], d, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) inner[i][j][r] = fmaf(s[i], d[r], inner[i][j][r]);
                 }
