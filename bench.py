@@ -584,7 +584,7 @@ def run_prefill(args):
     cpu = None if args.no_cpu else run_cpu_prefill()
     return {"workload": "config5: 512-token prefill GEMM, X 512x4096 vs W_gate|W_up 14336x4096 (one launch) then "
                         "512x14336 vs W_down 4096x14336; one hipGraph of all timed steps, 3 rotated weight copies",
-            "dtype": "q4_0 x f32 on fp16 MFMA (exact q-8 operand, x as fp16 hi + lo*2^11, fp32 accumulate)",
+            "dtype": "q4_0 x f32 on fp16 MFMA (exact q-8 operand, x as fp16 hi + fp16 lo (x - hi), fp32 accumulate)",
             "ms_per_step": round(ms_step, 4), "steps": steps, "tokens_per_s": round(T / (ms_step * 1e-3), 1),
             "useful_flop_per_step": PREFILL_FLOP, "TFLOP_s": round(tflops, 1),
             "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS,

@@ -325,7 +325,9 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         for (int j = 0; j < WBL; ++j) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
             const uint32_t r = idx / kKB, kb = idx % kKB;
-            *reinterpret_cast<u4v*>(&lw[buf][r][kb][0]) = gq[j];
+            // the two blocks of a row swap slots in rows with bit 2 set, so
+            // the per-lane reads of 16 rows spread over all 32 banks
+            *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[j];
             ls[buf][r][kb] = gs[j];
         }
     };
@@ -356,7 +358,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 64 * wm + 16 * i + lr;
-                B[i] = unpack8(lw[buf][r][kb][lq]);
+                B[i] = unpack8(lw[buf][r][kb ^ ((r >> 2) & 1)][lq]);
                 s[i] = ls[buf][r][kb];
             }
             // One token subtile at a time: its hi and lo parts, then the 4
