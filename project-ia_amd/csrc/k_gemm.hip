@@ -29,12 +29,15 @@
 // in steps of 2 blocks staged in LDS (double-buffered, one barrier per
 // step): X hi/lo as fp16 rows padded to 144 bytes (conflict-free 16-byte
 // reads), W as raw 16-byte nibble blocks + scales, dequantized per lane
-// right before the MFMA.  Workgroups are ordered so that each XCD keeps one
-// token tile of X resident in its L2 and streams the weight rows.
+// right before the MFMA.  Global loads run ahead of the LDS stages: X one
+// step (L2 hits), the weight blocks two steps (HBM latency).  Workgroups are
+// ordered so that each XCD keeps one token tile of X resident in its L2 and
+// streams the weight rows.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "qh_kernels.hpp"
 #include "qh_vec.hpp"
@@ -283,13 +286,17 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.w[sg], 0, (int)(M * row_bytes), kBufFlagsG);
 
-    // ---- global -> register staging of one K-step ----
+    // ---- global -> register staging ----
+    // X of step k is loaded one step ahead (it is served by L2); the weight
+    // blocks of step k two steps ahead, into register set k & 1, so that
+    // their HBM latency has two steps of compute to hide behind.  Within a
+    // step the X loads are issued first: the wait before the LDS store then
+    // leaves the newest weight loads in flight.
     u4v gx[XCH];
-    u4v gq[WBL];
-    float gs[WBL];
-    auto load_step = [&](uint32_t step) {
-        const uint32_t b0 = b_begin + step * kKB;
-        const uint32_t k0 = b0 * 32u;  // < N_pad - 63 by construction (N_pad % 64 == 0)
+    u4v gq[2][WBL];
+    float gs[2][WBL];
+    auto load_x = [&](uint32_t step) {
+        const uint32_t k0 = (b_begin + step * kKB) * 32u;  // < N_pad - 63 by construction (N_pad % 64 == 0)
 #pragma unroll
         for (int c = 0; c < XCH; ++c) {
             const uint32_t idx = (uint32_t)(tid + NT * c);
@@ -299,20 +306,26 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
             const _Float16* src = (part ? a.xl : a.xh) + (size_t)(t0 + t) * a.N_pad + k0 + 8u * ch;
             gx[c] = *reinterpret_cast<const u4v*>(src);
         }
+    };
+    auto load_w = [&](uint32_t step, auto setc) {
+        constexpr int set = decltype(setc)::value;
+        const uint32_t b0 = b_begin + step * kKB;
 #pragma unroll
         for (int j = 0; j < WBL; ++j) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
             const uint32_t r = idx / kKB, kb = idx % kKB;
             const uint32_t b = b0 + kb;
             const uint32_t off = (m0 + r) * row_bytes + b * 20u;  // rows >= M read zeros
-            u4v q = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
-            float s = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, off + 16u, 0, 0));
-            const bool ok = b < b_end;
-            gq[j] = ok ? q : u4v{0u, 0u, 0u, 0u};
-            gs[j] = ok ? s : 0.0f;
+            // Blocks past the split's end are masked at the LDS store (a
+            // select here would wait for the load right away).
+            gq[set][j] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+            gs[set][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, off + 16u, 0, 0));
         }
     };
-    auto store_step = [&](int buf) {
+    // LDS buffer `buf` (also the weight register set) <- the staged step.
+    auto store_step = [&](uint32_t step, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const uint32_t b0 = b_begin + step * kKB;
 #pragma unroll
         for (int c = 0; c < XCH; ++c) {
             const uint32_t idx = (uint32_t)(tid + NT * c);
@@ -327,10 +340,13 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
             const uint32_t r = idx / kKB, kb = idx % kKB;
             // the two blocks of a row swap slots in rows with bit 2 set, so
             // the per-lane reads of 16 rows spread over all 32 banks
-            *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[j];
-            ls[buf][r][kb] = gs[j];
+            // A zero scale removes a masked block: its products are finite.
+            *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[buf][j];
+            ls[buf][r][kb] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
         }
     };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
 
     f4v inner[4][4], outer[4][4];
 #pragma unroll
@@ -343,14 +359,19 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 
     const int lr = lane & 15, lq = lane >> 4;
     if (nsteps > 0) {
-        load_step(0);
-        store_step(0);
+        load_x(0);
+        load_w(0, I0{});
+        if (nsteps > 1) load_w(1, I1{});
+        store_step(0, I0{});
     }
     __syncthreads();
     uint32_t nb_in = 0;  // blocks in the current inner sum
-    for (uint32_t step = 0; step < nsteps; ++step) {
-        const int buf = step & 1;
-        if (step + 1 < nsteps) load_step(step + 1);
+    // One K-step from LDS buffer `buf` (= step & 1).
+    auto step_body = [&](uint32_t step, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        using Next = std::integral_constant<int, buf ^ 1>;
+        if (step + 1 < nsteps) load_x(step + 1);
+        if (step + 2 < nsteps) load_w(step + 2, bufc);  // set buf held step's weights, now in LDS
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
             h8v B[4];
@@ -388,8 +409,12 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                 }
             nb_in = 0;
         }
-        if (step + 1 < nsteps) store_step(buf ^ 1);
+        if (step + 1 < nsteps) store_step(step + 1, Next{});
         __syncthreads();
+    };
+    for (uint32_t step = 0; step < nsteps; step += 2) {
+        step_body(step, I0{});
+        if (step + 1 < nsteps) step_body(step + 1, I1{});
     }
 
     // ---- epilogue: lane holds column m (weight row), tokens 4*lq + r ----
