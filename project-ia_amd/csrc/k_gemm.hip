@@ -226,18 +226,30 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, uint32_t sg, uint3
     a.y[sg][i] = mt.y != 0.0f ? __builtin_nanf("") : y;
 }
 
-// 8 nibbles of one dword -> 8 fp16 (q - 8), in the kPerm order.
-__device__ __forceinline__ h8v unpack8(uint32_t w) {
-    h8v r;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t b = ((w >> (4 * c)) & 0x000F000Fu) | 0x64006400u;  // (1024 + n_c, 1024 + n_{c+4})
-        h2v h = __builtin_bit_cast(h2v, b);
-        h = h - h2v{(_Float16)1032.0f, (_Float16)1032.0f};
-        r[2 * c] = h[0];
-        r[2 * c + 1] = h[1];
-    }
+// (a & mask) | c in one instruction (the compiler splits it in two when both
+// constants are literals).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(c));
     return r;
+}
+
+// 8 nibbles of one dword -> 8 fp16 (q - 8), in the perm8 order: half pairs
+// (n_c, n_{c+4}) for c = 0..3.  A nibble OR'ed under the fp16 bit pattern of
+// 1024 gives 1024 + n (bits 0-3) or 1024 + 16 n (bits 4-7); the first is
+// shifted by -1032, the second scaled by 1/16 and shifted by -72 (every step
+// exact in fp16).  Nibbles 2, 3, 6, 7 take the same two forms after a shift
+// by 8.
+__device__ __forceinline__ h8v unpack8(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    const h2v lo_shift = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const h2v hi_scale = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2v hi_shift = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const h2v p0 = __builtin_bit_cast(h2v, and_or(w, 0x000F000Fu, 0x64006400u)) + lo_shift;
+    const h2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, and_or(w, 0x00F000F0u, 0x64006400u)), hi_scale, hi_shift);
+    const h2v p2 = __builtin_bit_cast(h2v, and_or(w8, 0x000F000Fu, 0x64006400u)) + lo_shift;
+    const h2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, and_or(w8, 0x00F000F0u, 0x64006400u)), hi_scale, hi_shift);
+    return h8v{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 template <int WM, int WT>
@@ -295,17 +307,21 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     u4v gx[XCH];
     u4v gq[2][WBL];
     float gs[2][WBL];
+    // The thread's X chunks (row t0 + t, 8 halfs at column 8*ch of the step)
+    // as pointers fixed for the whole loop.
+    const _Float16* xsrc[XCH];
+#pragma unroll
+    for (int c = 0; c < XCH; ++c) {
+        const uint32_t idx = (uint32_t)(tid + NT * c);
+        const uint32_t part = idx / (8u * BT);
+        const uint32_t rem = idx % (8u * BT);
+        const uint32_t t = rem / 8u, ch = rem % 8u;
+        xsrc[c] = (part ? a.xl : a.xh) + (size_t)(t0 + t) * a.N_pad + 8u * ch;
+    }
     auto load_x = [&](uint32_t step) {
         const uint32_t k0 = (b_begin + step * kKB) * 32u;  // < N_pad - 63 by construction (N_pad % 64 == 0)
 #pragma unroll
-        for (int c = 0; c < XCH; ++c) {
-            const uint32_t idx = (uint32_t)(tid + NT * c);
-            const uint32_t part = idx / (8u * BT);
-            const uint32_t rem = idx % (8u * BT);
-            const uint32_t t = rem / 8u, ch = rem % 8u;
-            const _Float16* src = (part ? a.xl : a.xh) + (size_t)(t0 + t) * a.N_pad + k0 + 8u * ch;
-            gx[c] = *reinterpret_cast<const u4v*>(src);
-        }
+        for (int c = 0; c < XCH; ++c) gx[c] = *reinterpret_cast<const u4v*>(xsrc[c] + k0);
     };
     auto load_w = [&](uint32_t step, auto setc) {
         constexpr int set = decltype(setc)::value;
@@ -370,8 +386,11 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     auto step_body = [&](uint32_t step, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
         using Next = std::integral_constant<int, buf ^ 1>;
-        if (step + 1 < nsteps) load_x(step + 1);
-        if (step + 2 < nsteps) load_w(step + 2, bufc);  // set buf held step's weights, now in LDS
+        // Issued unconditionally (the last steps reload step nsteps - 1, which
+        // is never stored): a load issued on one path only would make the wait
+        // before the LDS store cover the newest weight loads as well.
+        load_x(min(step + 1, nsteps - 1));
+        load_w(min(step + 2, nsteps - 1), bufc);  // set buf held step's weights, now in LDS
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
             h8v B[4];
