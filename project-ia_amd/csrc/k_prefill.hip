@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "qh_prefill.hpp"
 #include "qh_vec.hpp"
@@ -83,10 +84,13 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 // ---------------------------------------------------------------------------
 // Causal prefill attention on v_mfma_f32_16x16x4_f32.
 //
-// Workgroup: 16 queries (a query tile) x the G query heads of one KV head,
-// two waves per head, each taking half of every staged 64-key block (so a
-// tile's serial chain is half its keys); the 2G waves share the key/value
-// rows, staged in LDS 64 keys at a time.  Per query (as in the decode step):
+// Workgroup: 16 queries (a query tile) x HG of the G query heads of one KV
+// head, two waves per head, each taking half of every staged 64-key block (so
+// a tile's serial chain is half its keys); the 2HG waves share the key/value
+// rows, staged in LDS 64 keys at a time, the next block's rows loading into
+// registers while the current one is used.  G/HG workgroups share a (query
+// tile, KV head): more, smaller workgroups even out the causal triangle's
+// unequal tiles over the CUs.  Per query (as in the decode step):
 // s_j = (q . k_j) * scale for j <= P (its position), m = max_j s_j,
 // e_j = exp_approx(s_j - m) for j < (P+1) & ~7 and expf above (all expf when
 // P+1 < 8), o = sum_j e_j v_j times 1/sum_j e_j (divided by the sum when
@@ -111,22 +115,26 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
 
-template <uint32_t G>
-__global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs a) {
-    constexpr uint32_t NT = 128 * G;
+template <uint32_t G, uint32_t HG>
+__global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs a) {
+    static_assert(G % HG == 0, "head split");
+    constexpr uint32_t NT = 128 * HG;
     constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
     static_assert(kLoads * NT == kAttnKS * (kPHd / 4), "stage/thread mismatch");
-    static_assert(G * 64 * 32 <= 2 * kAttnKS * kAttnRS, "the P.V exchange reuses the staging space");
+    static_assert(HG * 64 * 32 <= 2 * kAttnKS * kAttnRS, "the P.V exchange reuses the staging space");
     __shared__ __attribute__((aligned(16))) float lkv[2][kAttnKS][kAttnRS];  // [0] K rows, [1] V rows
-    __shared__ float xmax[2][G][16], xsum[G][16];
+    __shared__ float xmax[2][HG][16], xsum[HG][16];
 
     const uint32_t n_qt = (a.T + 15) / 16;
-    const uint32_t qt = n_qt - 1 - blockIdx.x;  // the longest rows first
-    const uint32_t kvh = blockIdx.y;
+    // The first half of the grid takes the longest rows first, the second
+    // half the shortest first: a CU that holds workgroups b and b + half the
+    // grid then gets about the same number of keys as any other.
+    const uint32_t qt = (2 * blockIdx.y < gridDim.y) ? n_qt - 1 - blockIdx.x : blockIdx.x;
+    const uint32_t kvh = blockIdx.y / (G / HG), hs = blockIdx.y % (G / HG);
     const uint32_t t0 = qt * 16;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t hw = wave % G, half = wave / G;  // head within the group, half of each block
-    const uint32_t h = kvh * G + hw;
+    const uint32_t hw = wave % HG, half = wave / HG;  // head within the workgroup, half of each block
+    const uint32_t h = kvh * G + hs * HG + hw;
     const uint32_t li = lane & 15, lg = lane >> 4;
     const uint32_t t_last = min(t0 + 15u, a.T - 1u);
     const uint32_t n_keys = a.pos0 + t_last + 1u;  // keys of the tile's last query
@@ -154,10 +162,17 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
         }
     }
 
-    // Rows st*KS .. +KS-1 of K (and V) into LDS; rows past the tile's keys
-    // repeat its last key (in bounds; masked by j <= P below).
-    auto stage = [&](uint32_t st, bool with_v) {
-        float4 kr[kLoads], vr[kLoads];
+    // Rows st*KS .. +KS-1 of K (and V): fetch into registers, then put into
+    // LDS; rows past the tile's keys repeat its last key (in bounds; masked
+    // by j <= P below).
+    // (vectors rather than arrays: arrays live across the loop stayed in
+    // scratch memory)
+    typedef float stage_v __attribute__((ext_vector_type(4 * kLoads)));
+    stage_v kr, vr;
+    using NoV = std::false_type;
+    using WithV = std::true_type;
+    auto fetch = [&](uint32_t st, auto with_vc) {
+        constexpr bool with_v = decltype(with_vc)::value;
 #pragma unroll
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
@@ -165,15 +180,30 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
             uint32_t j = st * kAttnKS + r;
             j = j < n_keys ? j : n_keys - 1u;
             const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)j * 2 * kPHd) + c;
-            kr[u] = src[0];
-            if (with_v) vr[u] = src[kPHd / 4];
+            const float4 k4 = src[0];
+            kr[4 * u] = k4.x;
+            kr[4 * u + 1] = k4.y;
+            kr[4 * u + 2] = k4.z;
+            kr[4 * u + 3] = k4.w;
+            if constexpr (with_v) {
+                const float4 v4 = src[kPHd / 4];
+                vr[4 * u] = v4.x;
+                vr[4 * u + 1] = v4.y;
+                vr[4 * u + 2] = v4.z;
+                vr[4 * u + 3] = v4.w;
+            }
         }
+    };
+    auto put = [&](auto with_vc) {
+        constexpr bool with_v = decltype(with_vc)::value;
 #pragma unroll
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
-            *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) = kr[u];
-            if (with_v) *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) = vr[u];
+            *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) = make_float4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+            if constexpr (with_v)
+                *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) =
+                    make_float4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
         }
     };
 
@@ -200,10 +230,12 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
 
     // ---- pass 1: row max (this half's keys, then both halves) ----
     float mx = -INFINITY;
+    fetch(0, NoV{});
     for (uint32_t st = 0; st < n_stages; ++st) {
         __syncthreads();  // the previous stage's reads are done
-        stage(st, false);
+        put(NoV{});
         __syncthreads();
+        if (st + 1 < n_stages) fetch(st + 1, NoV{});
 #pragma unroll
         for (uint32_t s2 = 0; s2 < 2; ++s2) {
             const uint32_t sub = 2 * half + s2;
@@ -218,6 +250,7 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
             }
         }
     }
+    fetch(0, WithV{});  // pass 2's first block, in flight during the exchange
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     if (lane < 16) xmax[half][hw][lane] = mx;
@@ -231,8 +264,9 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
     float sum = 0.0f;
     for (uint32_t st = 0; st < n_stages; ++st) {
         __syncthreads();
-        stage(st, true);
+        put(WithV{});
         __syncthreads();
+        if (st + 1 < n_stages) fetch(st + 1, WithV{});
 #pragma unroll
         for (uint32_t s2 = 0; s2 < 2; ++s2) {
             const uint32_t sub = 2 * half + s2;
@@ -304,8 +338,9 @@ __global__ __launch_bounds__(128 * G) void k_prefill_attn(const PrefillAttnArgs 
 
 template <uint32_t G>
 static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
+    constexpr uint32_t HG = G < 2 ? G : 2;  // heads per workgroup
     const uint32_t n_qt = (a.T + 15) / 16;
-    hipLaunchKernelGGL(k_prefill_attn<G>, dim3(n_qt, a.n_kv), dim3(128 * G), 0, s, a);
+    hipLaunchKernelGGL((k_prefill_attn<G, HG>), dim3(n_qt, a.n_kv * (G / HG)), dim3(128 * HG), 0, s, a);
     return hipGetLastError();
 }
 
