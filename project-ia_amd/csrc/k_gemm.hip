@@ -190,7 +190,8 @@ struct GemmArgs {
     const uint8_t* w[kGemmMaxSeg];
     float* y[kGemmMaxSeg];
     const float* res[kGemmMaxSeg];  // optional residual rows added to y (same layout)
-    uint32_t M[kGemmMaxSeg];
+    uint32_t M[kGemmMaxSeg];        // weight rows (output columns) of the segment
+    uint32_t ld[kGemmMaxSeg];       // row length of y and res (the whole matrix's rows)
     uint32_t mt_end[kGemmMaxSeg];   // cumulative m-tile counts per segment
     uint32_t nseg;
     uint32_t nblk;        // blocks per weight row
@@ -220,7 +221,7 @@ __device__ __forceinline__ uint32_t seg_of_col(const GemmArgs& a, uint32_t c) {
 // operands: v * 2^-e, plus the residual when given; NaN for a non-finite row.
 __device__ __forceinline__ void gemm_store(const GemmArgs& a, uint32_t sg, uint32_t t, uint32_t m, float v) {
     const float2 mt = a.meta[t];
-    const size_t i = (size_t)t * a.M[sg] + m;
+    const size_t i = (size_t)t * a.ld[sg] + m;
     float y = v * mt.x;
     if (a.res[sg]) y = a.res[sg][i] + y;
     a.y[sg][i] = mt.y != 0.0f ? __builtin_nanf("") : y;
@@ -252,14 +253,18 @@ __device__ __forceinline__ h8v unpack8(uint32_t w) {
     return h8v{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-template <int WM, int WT>
+// MI: 16-row weight subtiles per wave (a wave's tile is 16*MI x 64).
+template <int WM, int WT, int MI>
 __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     constexpr int NT = 64 * WM * WT;
-    constexpr int BM = 64 * WM;
+    constexpr int WR = 16 * MI;  // weight rows per wave
+    constexpr int BM = WR * WM;
     constexpr int BT = 64 * WT;
-    constexpr int XCH = 16 * BT / NT;   // 16-byte X chunks per thread per K-step
-    constexpr int WBL = BM * kKB / NT;  // weight blocks per thread per K-step
-    static_assert(XCH * NT == 16 * BT && WBL * NT == BM * kKB, "tile/thread mismatch");
+    constexpr int XCH = 16 * BT / NT;                 // 16-byte X chunks per thread per K-step
+    constexpr int WBL = (BM * kKB + NT - 1) / NT;     // weight blocks per thread per K-step
+    constexpr bool kWAll = WBL * NT == BM * kKB;      // every thread stages WBL blocks
+    static_assert(XCH * NT == 16 * BT, "tile/thread mismatch");
+    static_assert(BM * kKB % 64 == 0, "weight staging threads come in whole waves");
 
     __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BT][kXRow];
     __shared__ __attribute__((aligned(16))) uint32_t lw[2][BM][kKB][4];
@@ -331,7 +336,9 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
             const uint32_t r = idx / kKB, kb = idx % kKB;
             const uint32_t b = b0 + kb;
-            const uint32_t off = (m0 + r) * row_bytes + b * 20u;  // rows >= M read zeros
+            // rows >= M read zeros; threads past the tile's blocks (kWAll
+            // false) load some row of the buffer and store nothing
+            const uint32_t off = (m0 + r) * row_bytes + b * 20u;
             // Blocks past the split's end are masked at the LDS store (a
             // select here would wait for the load right away).
             gq[set][j] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
@@ -354,19 +361,21 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         for (int j = 0; j < WBL; ++j) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
             const uint32_t r = idx / kKB, kb = idx % kKB;
-            // the two blocks of a row swap slots in rows with bit 2 set, so
-            // the per-lane reads of 16 rows spread over all 32 banks
-            // A zero scale removes a masked block: its products are finite.
-            *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[buf][j];
-            ls[buf][r][kb] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
+            if (kWAll || idx < (uint32_t)(BM * kKB)) {  // wave-uniform: BM * kKB is a multiple of 64
+                // the two blocks of a row swap slots in rows with bit 2 set, so
+                // the per-lane reads of 16 rows spread over all 32 banks
+                // A zero scale removes a masked block: its products are finite.
+                *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[buf][j];
+                ls[buf][r][kb] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
+            }
         }
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
 
-    f4v inner[4][4], outer[4][4];
+    f4v inner[MI][4], outer[MI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             inner[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -393,15 +402,15 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         load_w(min(step + 2, nsteps - 1), bufc);  // set buf held step's weights, now in LDS
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
-            h8v B[4];
-            float s[4];
+            h8v B[MI];
+            float s[MI];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 64 * wm + 16 * i + lr;
+            for (int i = 0; i < MI; ++i) {
+                const int r = WR * wm + 16 * i + lr;
                 B[i] = unpack8(lw[buf][r][kb ^ ((r >> 2) & 1)][lq]);
                 s[i] = ls[buf][r][kb];
             }
-            // One token subtile at a time: its hi and lo parts, then the 4
+            // One token subtile at a time: its hi and lo parts, then the MI
             // weight subtiles.
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                 const h8v Ah = *reinterpret_cast<const h8v*>(&lx[buf][0][t][32 * kb + 8 * lq]);
                 const h8v Al = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < MI; ++i) {
                     f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B[i], d, 0, 0, 0);
 #pragma unroll
@@ -420,7 +429,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         nb_in += kKB;
         if (nb_in >= kInner) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     outer[i][j] += inner[i][j];
@@ -438,8 +447,8 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 
     // ---- epilogue: lane holds column m (weight row), tokens 4*lq + r ----
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t m = m0 + 64 * wm + 16 * i + lr;
+    for (int i = 0; i < MI; ++i) {
+        const uint32_t m = m0 + WR * wm + 16 * i + lr;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const f4v v = outer[i][j] + inner[i][j];
@@ -499,6 +508,33 @@ size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
     return b;
 }
 
+// Arguments for rows [r0, r1) of the segments laid end to end, in m-tiles of
+// `bm` rows (a range may cut segments: its pieces point into them).
+static void gemm_rows_args(GemmArgs& a, const GemmSegs& sg, uint32_t r0, uint32_t r1, uint32_t bm,
+                           uint32_t row_bytes) {
+    uint32_t base = 0, mt = 0, n = 0;
+    for (int i = 0; i < sg.n; ++i) {
+        const uint32_t lo = std::max(r0, base), hi = std::min(r1, base + sg.M[i]);
+        if (lo < hi) {
+            const uint32_t off = lo - base;
+            a.w[n] = sg.w[i] + (size_t)off * row_bytes;
+            a.y[n] = sg.y[i] + off;
+            a.res[n] = sg.res[i] ? sg.res[i] + off : nullptr;
+            a.M[n] = hi - lo;
+            a.ld[n] = sg.M[i];
+            mt += (hi - lo + bm - 1) / bm;
+            a.mt_end[n] = mt;
+            ++n;
+        }
+        base += sg.M[i];
+    }
+    a.nseg = n;
+}
+
+// Workgroup rounds of the whole GPU (256 CUs, one workgroup each) for
+// `wgs` workgroups.
+static uint32_t gemm_rounds(uint32_t wgs) { return (wgs + 255u) / 256u; }
+
 hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipStream_t s) {
     const uint32_t N = in.N, T = in.T;
     const int nseg = sg.n;
@@ -506,6 +542,7 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     if (gemm_npad(N) > 8u * 256u * kXpMaxGroups) return hipErrorInvalidValue;  // the row conversion's register tile
     if (in.norm_w && in.u) return hipErrorInvalidValue;
     const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
+    const uint32_t row_bytes = (N / 32u) * 20u;
     uint8_t* p = static_cast<uint8_t*>(ws);
     const size_t plane = align256((size_t)tp * np * 2);
     GemmArgs a{};
@@ -516,11 +553,12 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     uint32_t mt = 0, mtot = 0;
     for (int i = 0; i < nseg; ++i) {
         // Weight offsets are 32-bit buffer offsets.
-        if (sg.M[i] == 0 || (uint64_t)sg.M[i] * (N / 32u) * 20u >= (1ull << 31)) return hipErrorInvalidValue;
+        if (sg.M[i] == 0 || (uint64_t)sg.M[i] * row_bytes >= (1ull << 31)) return hipErrorInvalidValue;
         a.w[i] = sg.w[i];
         a.y[i] = sg.y[i];
         a.res[i] = sg.res[i];
         a.M[i] = sg.M[i];
+        a.ld[i] = sg.M[i];
         a.part_off[i] = mtot;
         mtot += sg.M[i];
         mt += (sg.M[i] + kGemmBM - 1) / kGemmBM;
@@ -546,9 +584,42 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
                        const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t pairs = mt * a.split * a.n_tt;
-    const uint32_t grid = a.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
-    hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, a);
+    auto grid_of = [&](const GemmArgs& g) {
+        const uint32_t pairs = g.mt_end[g.nseg - 1] * g.split * g.n_tt;
+        return g.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
+    };
+    if (a.split == 1) {
+        // Whole-K tiles: when the 256-row tiles leave the last round of
+        // workgroups part-empty, the rows after the first r256 go to 192-row
+        // tiles (3/4 of the work each) in a second launch, chosen to make the
+        // fewest rounds (counted in 256-row units).
+        const uint32_t n_tt = a.n_tt;
+        const uint32_t full = gemm_rounds((mtot + 255u) / 256u * n_tt) * 4u;
+        uint32_t best = full, best_r = mtot;
+        for (uint32_t r = 0; r < mtot; r += 256u) {
+            const uint32_t c = gemm_rounds(r / 256u * n_tt) * 4u + gemm_rounds((mtot - r + 191u) / 192u * n_tt) * 3u;
+            if (c < best) {
+                best = c;
+                best_r = r;
+            }
+        }
+        if (best_r < mtot) {
+            if (best_r > 0) {
+                GemmArgs a1 = a;
+                gemm_rows_args(a1, sg, 0, best_r, 256u, row_bytes);
+                hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid_of(a1)), dim3(64 * kGemmWM * kGemmWT),
+                                   0, s, a1);
+                e = hipGetLastError();
+                if (e != hipSuccess) return e;
+            }
+            GemmArgs a2 = a;
+            gemm_rows_args(a2, sg, best_r, mtot, 192u, row_bytes);
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 3>), dim3(grid_of(a2)), dim3(64 * kGemmWM * kGemmWT), 0,
+                               s, a2);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid_of(a)), dim3(64 * kGemmWM * kGemmWT), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || a.split == 1) return e;
     const size_t n = (size_t)T * mtot;
