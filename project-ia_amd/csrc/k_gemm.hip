@@ -484,25 +484,81 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kGemmWM = 4, kGemmWT = 2;
-constexpr uint32_t kGemmBM = 64 * kGemmWM, kGemmBT = 64 * kGemmWT;
+constexpr uint32_t kGemmBT = 64 * kGemmWT;  // token rows per tile
 
 static uint32_t gemm_tpad(uint32_t T) { return (T + kGemmBT - 1) / kGemmBT * kGemmBT; }
 static uint32_t gemm_npad(uint32_t N) { return (N + 63u) & ~63u; }
 
-// K splits: enough (m-tile, token-tile, split) workgroups to cover the 256
-// CUs, each split keeping at least 32 blocks.
-static uint32_t gemm_split(uint32_t M_total, uint32_t T, uint32_t nblk) {
-    const uint32_t tiles = (M_total + kGemmBM - 1) / kGemmBM * (gemm_tpad(T) / kGemmBT);
-    uint32_t s = 1;
-    while (tiles * s < 256u && s < 8u && nblk / (2u * s) >= 32u) s *= 2u;
-    return s;
+// Launch plan of a GEMM over weight matrices of Ms[0..nseg) rows (each tiled
+// on its own), T tokens and nblk blocks per row: the tile height (256 or 192
+// rows), the K split (partials plus a reduction pass when > 1; each split
+// keeps at least 32 blocks, and at most max_split), and, for whole-K
+// launches, a cut: rows from `cut` on (counted over the matrices laid end to
+// end) run in 192-row tiles in a second launch.  The cost model is measured
+// on MI355X at T = 512: a launch takes rounds x (16 us + K-steps x 2.12 us
+// for 256-row tiles, 1.66 us for 192-row tiles), a round being up to 256
+// workgroups (one per CU); a reduction about 1 us plus its traffic at 5 TB/s.
+struct GemmPlan {
+    uint32_t bm;     // tile height of the (first) launch
+    uint32_t split;
+    uint32_t cut;    // the total row count: one launch
+};
+
+static uint32_t gemm_rounds(uint32_t wgs) { return (wgs + 255u) / 256u; }
+
+static GemmPlan gemm_plan(const uint32_t* Ms, int nseg, uint32_t T, uint32_t nblk, uint32_t max_split) {
+    const uint32_t n_tt = gemm_tpad(T) / kGemmBT;
+    uint32_t mtot = 0;
+    for (int i = 0; i < nseg; ++i) mtot += Ms[i];
+    auto steps_of = [&](uint32_t sp) { return ((nblk + sp - 1) / sp + kKB - 1) / kKB; };
+    // m-tiles of rows [r0, r1) of the matrices laid end to end
+    auto tiles = [&](uint32_t r0, uint32_t r1, uint32_t bm) {
+        uint32_t base = 0, n = 0;
+        for (int i = 0; i < nseg; ++i) {
+            const uint32_t lo = std::max(r0, base), hi = std::min(r1, base + Ms[i]);
+            if (lo < hi) n += (hi - lo + bm - 1) / bm;
+            base += Ms[i];
+        }
+        return n;
+    };
+    auto launch_us = [&](uint32_t wgs, uint32_t bm, uint32_t steps) {
+        return gemm_rounds(wgs) * (16.0 + steps * (bm == 256u ? 2.12 : 1.66));
+    };
+    GemmPlan best{256u, 1u, mtot};
+    double best_c = 1e30;
+    for (uint32_t bm : {256u, 192u}) {
+        for (uint32_t sp = 1; sp <= max_split; sp *= 2u) {
+            if (sp > 1 && nblk / sp < 32u) break;
+            double c = launch_us(tiles(0, mtot, bm) * n_tt * sp, bm, steps_of(sp));
+            if (sp > 1) c += 1.0 + (double)(sp + 1) * T * mtot * 4.0 / 5e6;
+            if (c < best_c) {
+                best_c = c;
+                best = GemmPlan{bm, sp, mtot};
+            }
+        }
+    }
+    for (uint32_t r = 256u; r < mtot; r += 256u) {
+        const double c = launch_us(tiles(0, r, 256u) * n_tt, 256u, steps_of(1)) +
+                         launch_us(tiles(r, mtot, 192u) * n_tt, 192u, steps_of(1));
+        if (c < best_c) {
+            best_c = c;
+            best = GemmPlan{256u, 1u, r};
+        }
+    }
+    return best;
+}
+
+// The K split a workspace is sized for: the plan of M_total rows as one
+// matrix (a launch over several matrices takes at most this split).
+static uint32_t gemm_ws_split(uint32_t M_total, uint32_t T, uint32_t nblk) {
+    return gemm_plan(&M_total, 1, T, nblk, 8u).split;
 }
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t gemm_workspace_bytes(uint32_t N, uint32_t T, uint32_t M_total) {
     const size_t tp = gemm_tpad(T), np = gemm_npad(N);
-    const uint32_t sp = gemm_split(M_total, T, N / 32u);
+    const uint32_t sp = gemm_ws_split(M_total, T, N / 32u);
     size_t b = 2 * align256(tp * np * 2) + align256(tp * 8);
     if (sp > 1) b += align256((size_t)sp * T * M_total * 4);
     return b;
@@ -531,10 +587,6 @@ static void gemm_rows_args(GemmArgs& a, const GemmSegs& sg, uint32_t r0, uint32_
     a.nseg = n;
 }
 
-// Workgroup rounds of the whole GPU (256 CUs, one workgroup each) for
-// `wgs` workgroups.
-static uint32_t gemm_rounds(uint32_t wgs) { return (wgs + 255u) / 256u; }
-
 hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipStream_t s) {
     const uint32_t N = in.N, T = in.T;
     const int nseg = sg.n;
@@ -550,26 +602,19 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     a.xl = reinterpret_cast<_Float16*>(p + plane);
     a.meta = reinterpret_cast<float2*>(p + 2 * plane);
     float* part = reinterpret_cast<float*>(p + 2 * plane + align256((size_t)tp * 8));
-    uint32_t mt = 0, mtot = 0;
+    uint32_t mtot = 0;
     for (int i = 0; i < nseg; ++i) {
         // Weight offsets are 32-bit buffer offsets.
         if (sg.M[i] == 0 || (uint64_t)sg.M[i] * row_bytes >= (1ull << 31)) return hipErrorInvalidValue;
-        a.w[i] = sg.w[i];
-        a.y[i] = sg.y[i];
-        a.res[i] = sg.res[i];
-        a.M[i] = sg.M[i];
-        a.ld[i] = sg.M[i];
         a.part_off[i] = mtot;
         mtot += sg.M[i];
-        mt += (sg.M[i] + kGemmBM - 1) / kGemmBM;
-        a.mt_end[i] = mt;
     }
-    a.nseg = (uint32_t)nseg;
+    const GemmPlan plan = gemm_plan(sg.M, nseg, T, N / 32u, gemm_ws_split(mtot, T, N / 32u));
     a.nblk = N / 32;
     a.T = T;
     a.N_pad = np;
     a.n_tt = tp / kGemmBT;
-    a.split = gemm_split(mtot, T, a.nblk);
+    a.split = plan.split;
     a.blk_per_split = ((a.nblk + a.split - 1) / a.split + kKB - 1) / kKB * kKB;
     a.part = part;
     a.part_ld = mtot;
@@ -584,44 +629,27 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
                        const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    auto grid_of = [&](const GemmArgs& g) {
+    // rows [r0, r1) in tiles of bm rows
+    auto launch = [&](uint32_t r0, uint32_t r1, uint32_t bm) -> hipError_t {
+        GemmArgs g = a;
+        gemm_rows_args(g, sg, r0, r1, bm, row_bytes);
         const uint32_t pairs = g.mt_end[g.nseg - 1] * g.split * g.n_tt;
-        return g.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
+        const uint32_t grid = g.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
+        if (bm == 256u)
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, g);
+        else
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 3>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, g);
+        return hipGetLastError();
     };
-    if (a.split == 1) {
-        // Whole-K tiles: when the 256-row tiles leave the last round of
-        // workgroups part-empty, the rows after the first r256 go to 192-row
-        // tiles (3/4 of the work each) in a second launch, chosen to make the
-        // fewest rounds (counted in 256-row units).
-        const uint32_t n_tt = a.n_tt;
-        const uint32_t full = gemm_rounds((mtot + 255u) / 256u * n_tt) * 4u;
-        uint32_t best = full, best_r = mtot;
-        for (uint32_t r = 0; r < mtot; r += 256u) {
-            const uint32_t c = gemm_rounds(r / 256u * n_tt) * 4u + gemm_rounds((mtot - r + 191u) / 192u * n_tt) * 3u;
-            if (c < best) {
-                best = c;
-                best_r = r;
-            }
-        }
-        if (best_r < mtot) {
-            if (best_r > 0) {
-                GemmArgs a1 = a;
-                gemm_rows_args(a1, sg, 0, best_r, 256u, row_bytes);
-                hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid_of(a1)), dim3(64 * kGemmWM * kGemmWT),
-                                   0, s, a1);
-                e = hipGetLastError();
-                if (e != hipSuccess) return e;
-            }
-            GemmArgs a2 = a;
-            gemm_rows_args(a2, sg, best_r, mtot, 192u, row_bytes);
-            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 3>), dim3(grid_of(a2)), dim3(64 * kGemmWM * kGemmWT), 0,
-                               s, a2);
-            return hipGetLastError();
-        }
+    if (plan.cut < mtot) {
+        e = launch(0, plan.cut, 256u);
+        if (e != hipSuccess) return e;
+        return launch(plan.cut, mtot, 192u);
     }
-    hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid_of(a)), dim3(64 * kGemmWM * kGemmWT), 0, s, a);
-    e = hipGetLastError();
+    e = launch(0, mtot, plan.bm);
     if (e != hipSuccess || a.split == 1) return e;
+    // the reduction reads the partials by column of the whole row set
+    gemm_rows_args(a, sg, 0, mtot, plan.bm, row_bytes);
     const size_t n = (size_t)T * mtot;
     const uint32_t rg = (uint32_t)std::min<size_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(k_gemm_reduce, dim3(rg), dim3(256), 0, s, a);
