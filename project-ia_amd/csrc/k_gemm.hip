@@ -227,6 +227,24 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, uint32_t sg, uint3
     a.y[sg][i] = mt.y != 0.0f ? __builtin_nanf("") : y;
 }
 
+// gemm_store of rows m .. m+3 (those below the segment's M), with 16-byte
+// accesses where the row length keeps them aligned.
+__device__ __forceinline__ void gemm_store4(const GemmArgs& a, uint32_t sg, uint32_t t, uint32_t m, f4v v) {
+    const uint32_t M = a.M[sg];
+    if ((a.ld[sg] & 3u) != 0 || m + 3 >= M) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (m + r < M) gemm_store(a, sg, t, m + r, v[r]);
+        return;
+    }
+    const float2 mt = a.meta[t];
+    const size_t i = (size_t)t * a.ld[sg] + m;
+    f4v y = v * mt.x;
+    if (a.res[sg]) y = *reinterpret_cast<const f4v*>(a.res[sg] + i) + y;
+    if (mt.y != 0.0f) y = f4v{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+    *reinterpret_cast<f4v*>(a.y[sg] + i) = y;
+}
+
 // (a & mask) | c in one instruction (the compiler splits it in two when both
 // constants are literals).
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t c) {
@@ -268,7 +286,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 
     __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BT][kXRow];
     __shared__ __attribute__((aligned(16))) uint32_t lw[2][BM][kKB][4];
-    __shared__ float ls[2][BM][kKB];
+    __shared__ __attribute__((aligned(16))) float ls[2][kKB][BM];
 
     // ---- tile of this workgroup ----
     const uint32_t n_mt = a.mt_end[a.nseg - 1] * a.split;  // (m-tile, split) pairs
@@ -366,7 +384,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                 // the per-lane reads of 16 rows spread over all 32 banks
                 // A zero scale removes a masked block: its products are finite.
                 *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[buf][j];
-                ls[buf][r][kb] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
+                ls[buf][kb][r] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
             }
         }
     };
@@ -402,13 +420,17 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         load_w(min(step + 2, nsteps - 1), bufc);  // set buf held step's weights, now in LDS
 #pragma unroll
         for (int kb = 0; kb < kKB; ++kb) {
+            // The weight fragment is the MFMA's A operand (D rows = weight
+            // rows, D columns = tokens): register r of lane l holds weight row
+            // 4*(l/16) + r of the subtile for token l%16, so each lane has 4
+            // consecutive outputs of one token row, and their 4 scales.
             h8v B[MI];
-            float s[MI];
+            f4v s[MI];
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const int r = WR * wm + 16 * i + lr;
                 B[i] = unpack8(lw[buf][r][kb ^ ((r >> 2) & 1)][lq]);
-                s[i] = ls[buf][r][kb];
+                s[i] = *reinterpret_cast<const f4v*>(&ls[buf][kb][WR * wm + 16 * i + 4 * lq]);
             }
             // One token subtile at a time: its hi and lo parts, then the MI
             // weight subtiles.
@@ -419,10 +441,10 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                 const h8v Al = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
 #pragma unroll
                 for (int i = 0; i < MI; ++i) {
-                    f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B[i], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B[i], d, 0, 0, 0);
+                    f4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(B[i], Ah, f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(B[i], Al, d, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) inner[i][j][r] = fmaf(s[i], d[r], inner[i][j][r]);
+                    for (int r = 0; r < 4; ++r) inner[i][j][r] = fmaf(s[i][r], d[r], inner[i][j][r]);
                 }
             }
         }
@@ -445,22 +467,26 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         if (step + 1 < nsteps) step_body(step + 1, I1{});
     }
 
-    // ---- epilogue: lane holds column m (weight row), tokens 4*lq + r ----
+    // ---- epilogue: lane holds weight rows m .. m+3 of token t ----
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-        const uint32_t m = m0 + WR * wm + 16 * i + lr;
+        const uint32_t m = m0 + WR * wm + 16 * i + 4 * lq;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+            const uint32_t t = t0 + 64 * wt + 16 * j + lr;
             const f4v v = outer[i][j] + inner[i][j];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t t = t0 + 64 * wt + 16 * j + 4 * lq + r;
-                if (m < M && t < a.T) {
-                    if (a.split > 1) {
-                        a.part[((size_t)sp * a.T + t) * a.part_ld + a.part_off[sg] + m] = v[r];
+            if (m < M && t < a.T) {
+                if (a.split > 1) {
+                    float* dst = a.part + ((size_t)sp * a.T + t) * a.part_ld + a.part_off[sg] + m;
+                    if ((a.part_ld & 3u) == 0 && (a.part_off[sg] & 3u) == 0 && m + 3 < M) {
+                        *reinterpret_cast<f4v*>(dst) = v;
                     } else {
-                        gemm_store(a, sg, t, m, v[r]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (m + r < M) dst[r] = v[r];
                     }
+                } else {
+                    gemm_store4(a, sg, t, m, v);
                 }
             }
         }
