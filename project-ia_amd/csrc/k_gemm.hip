@@ -75,6 +75,13 @@ struct GemmXIn {
     const float* u;       // SwiGLU mode when non-null
     const float* norm_w;  // RMSNorm mode when non-null
     float eps;
+    // Reduction mode when part is non-null: row t is
+    // (sum_s part[s][t]) * pmeta[t].x + res[t] (NaN where pmeta[t].y is set),
+    // the order of k_gemm_reduce and gemm_store, and is also written to x.
+    const float* part;
+    uint32_t split;
+    const float2* pmeta;
+    const float* res;
 };
 
 constexpr uint32_t kXpMaxGroups = 16;  // 8-element groups per thread: rows of up to 32768 elements
@@ -82,7 +89,7 @@ constexpr uint32_t kXpMaxGroups = 16;  // 8-element groups per thread: rows of u
 template <uint32_t kXpGroups>
 __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T, uint32_t N, uint32_t N_pad,
                                                     _Float16* __restrict__ xh, _Float16* __restrict__ xl,
-                                                    float2* __restrict__ meta) {
+                                                    float2* meta) {  // meta may be the producer's pmeta
     __shared__ float red[4];
     __shared__ int red_f[4];
     const uint32_t t = blockIdx.x;
@@ -93,13 +100,44 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T
     // The thread's groups g = tid + 256*i, read once (two 16-byte loads each).
     float v[kXpGroups][8];
     float ss = 0.0f;
+    // reduction mode: the producer's scale and flag of this row (read before
+    // the barriers that precede this kernel's own meta store)
+    const float2 pm = (in.part && valid) ? in.pmeta[t] : make_float2(1.0f, 0.0f);
+    const size_t pstride = (size_t)T * N / 4;  // float4s per partial plane
 #pragma unroll
     for (uint32_t i = 0; i < kXpGroups; ++i) {
         const uint32_t g = threadIdx.x + 256u * i;
         float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
         if (g < nv) {
-            a = x4[2 * g];
-            b = x4[2 * g + 1];
+            if (in.part) {
+                const float4* p4 = reinterpret_cast<const float4*>(in.part + (size_t)t * N);
+                a = p4[2 * g];
+                b = p4[2 * g + 1];
+                for (uint32_t sp = 1; sp < in.split; ++sp) {
+                    const float4 c = p4[sp * pstride + 2 * g], d = p4[sp * pstride + 2 * g + 1];
+                    a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+                    b.x += d.x; b.y += d.y; b.z += d.z; b.w += d.w;
+                }
+                a.x = a.x * pm.x; a.y = a.y * pm.x; a.z = a.z * pm.x; a.w = a.w * pm.x;
+                b.x = b.x * pm.x; b.y = b.y * pm.x; b.z = b.z * pm.x; b.w = b.w * pm.x;
+                if (in.res) {
+                    const float4* r4 = reinterpret_cast<const float4*>(in.res + (size_t)t * N);
+                    const float4 c = r4[2 * g], d = r4[2 * g + 1];
+                    a.x = c.x + a.x; a.y = c.y + a.y; a.z = c.z + a.z; a.w = c.w + a.w;
+                    b.x = d.x + b.x; b.y = d.y + b.y; b.z = d.z + b.z; b.w = d.w + b.w;
+                }
+                if (pm.y != 0.0f) {
+                    const float q = __builtin_nanf("");
+                    a = make_float4(q, q, q, q);
+                    b = a;
+                }
+                float4* o4 = reinterpret_cast<float4*>(const_cast<float*>(in.x) + (size_t)t * N);
+                o4[2 * g] = a;
+                o4[2 * g + 1] = b;
+            } else {
+                a = x4[2 * g];
+                b = x4[2 * g + 1];
+            }
         }
         v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
         v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
@@ -613,10 +651,13 @@ static void gemm_rows_args(GemmArgs& a, const GemmSegs& sg, uint32_t r0, uint32_
     a.nseg = n;
 }
 
-hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipStream_t s) {
+hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipStream_t s, GemmDeferred* defer_out) {
     const uint32_t N = in.N, T = in.T;
     const int nseg = sg.n;
-    if (nseg < 1 || nseg > kGemmMaxSeg || T == 0 || N == 0 || N % 32 != 0 || !in.x) return hipErrorInvalidValue;
+    if (defer_out) defer_out->valid = false;
+    const GemmDeferred* from = (in.from && in.from->valid) ? in.from : nullptr;
+    if (nseg < 1 || nseg > kGemmMaxSeg || T == 0 || N == 0 || N % 32 != 0 || !(in.x || from))
+        return hipErrorInvalidValue;
     if (gemm_npad(N) > 8u * 256u * kXpMaxGroups) return hipErrorInvalidValue;  // the row conversion's register tile
     if (in.norm_w && in.u) return hipErrorInvalidValue;
     const uint32_t tp = gemm_tpad(T), np = gemm_npad(N);
@@ -646,7 +687,18 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     a.part_ld = mtot;
     // The XCD-aware order needs the token-tile count to divide the 8 XCDs.
     a.xcd_map = (8u % a.n_tt == 0) ? 1u : 0u;
-    const GemmXIn xin{in.x, in.u, in.norm_w, in.eps};
+    GemmXIn xin{in.x, in.u, in.norm_w, in.eps, nullptr, 0u, nullptr, nullptr};
+    if (from) {
+        // The producer's partials lie beyond its own staged rows and scales;
+        // in a shared workspace this launch's rows and scales must end at or
+        // before those (a staged row no longer than the producer's).
+        if (from->T != T || from->M != N || (from->ws == ws && np > from->n_pad)) return hipErrorInvalidValue;
+        xin.x = from->y;
+        xin.part = from->part;
+        xin.split = from->split;
+        xin.pmeta = from->meta;
+        xin.res = from->res;
+    }
     // the smallest register tile holding the row: groups of 8 per thread
     const uint32_t per = (np / 8 + 255) / 256;
     auto xprep = per <= 2 ? k_gemm_xprep<2> : per <= 4 ? k_gemm_xprep<4> : per <= 8 ? k_gemm_xprep<8>
@@ -674,6 +726,20 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     }
     e = launch(0, mtot, plan.bm);
     if (e != hipSuccess || a.split == 1) return e;
+    if (defer_out && nseg == 1 && (mtot & 3u) == 0) {
+        // the next GEMM's row conversion sums the partials
+        defer_out->valid = true;
+        defer_out->part = part;
+        defer_out->split = a.split;
+        defer_out->T = T;
+        defer_out->M = mtot;
+        defer_out->meta = a.meta;
+        defer_out->res = sg.res[0];
+        defer_out->y = sg.y[0];
+        defer_out->ws = ws;
+        defer_out->n_pad = np;
+        return hipSuccess;
+    }
     // the reduction reads the partials by column of the whole row set
     gemm_rows_args(a, sg, 0, mtot, plan.bm, row_bytes);
     const size_t n = (size_t)T * mtot;

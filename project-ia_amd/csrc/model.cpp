@@ -397,6 +397,10 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         if (e != hipSuccess) return e;   \
     } while (0)
     QH_E(launch_embed_rows(p->embd, p->pf_tok, T, c.dim, p->pf_x, s));
+    // A split-K GEMM writing the residual stream (Wo, W_down) leaves its
+    // reduction to the next GEMM's row conversion (the RMSNorm before
+    // W_gate|W_up, and before the next layer's Q|K|V).
+    GemmDeferred pend;
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const LayerDev& L = p->layers[l];
         float* kvl = p->kv + (size_t)l * p->kv_layer_floats;
@@ -416,6 +420,7 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         xn.eps = c.rms_norm_eps;
         xn.T = T;
         xn.N = c.dim;
+        xn.from = &pend;
         QH_E(launch_gemm_ex(qkv, xn, p->pf_ws, s));
         QH_E(launch_rope_kv_rows(p->pf_q, p->pf_k, p->pf_v, p->cos_tab, p->sin_tab, pos0, T, c.n_heads,
                                  c.n_kv_heads, c.max_seq_len, kvl, s));
@@ -440,7 +445,7 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         on.x = p->pf_o;
         on.T = T;
         on.N = c.dim;
-        QH_E(launch_gemm_ex(wo, on, p->pf_ws, s));
+        QH_E(launch_gemm_ex(wo, on, p->pf_ws, s, &pend));
         GemmSegs gu;
         gu.n = 2;
         gu.w[0] = L.wg;
@@ -454,6 +459,7 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         x1n.eps = c.rms_norm_eps;
         x1n.T = T;
         x1n.N = c.dim;
+        x1n.from = &pend;
         QH_E(launch_gemm_ex(gu, x1n, p->pf_ws, s));
         GemmSegs wd;
         wd.n = 1;
@@ -466,7 +472,9 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         hn.u = p->pf_u;
         hn.T = T;
         hn.N = c.hidden_dim;
-        QH_E(launch_gemm_ex(wd, hn, p->pf_ws, s));
+        // the last layer's rows feed the LM head: reduced here
+        QH_E(launch_gemm_ex(wd, hn, p->pf_ws, s, l + 1 < c.n_layers ? &pend : nullptr));
+        if (l + 1 == c.n_layers) pend.valid = false;
     }
     if (last) {
         // LM head of RMSNorm(last row), as in the decode step.

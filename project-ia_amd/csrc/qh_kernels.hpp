@@ -101,14 +101,34 @@ struct GemmSegs {
     const float* res[3] = {};
     uint32_t M[3] = {};
 };
+// A one-matrix GEMM with a K split can leave its reduction to the next
+// GEMM's row conversion (launch_gemm_ex with defer_out): the partials, the
+// per-token scale and the residual are summed there in the reduction's own
+// order (bit-identical), the rows written to y, and then converted.  valid is
+// false when the launch had no split (y is then already written).
+struct GemmDeferred {
+    bool valid = false;
+    const float* part = nullptr;   // [split][T][M]
+    uint32_t split = 0, T = 0, M = 0;
+    const float2* meta = nullptr;  // the producer's per-token (2^-e, non-finite flag)
+    const float* res = nullptr;    // its residual rows [T][M] (or null)
+    float* y = nullptr;            // its output rows [T][M]
+    const void* ws = nullptr;      // its workspace and staged row length
+    uint32_t n_pad = 0;
+};
 struct GemmRows {
     const float* x = nullptr;       // [T][N]
     const float* u = nullptr;       // SwiGLU mode: [T][N] up rows
     const float* norm_w = nullptr;  // RMSNorm mode: [N] weight
     float eps = 0.0f;
     uint32_t T = 0, N = 0;
+    // When set and valid, the rows are the deferred producer's y (x unused):
+    // N must equal its M, and a shared workspace needs this GEMM's staged
+    // rows no longer than the producer's (its partials lie beyond them).
+    const GemmDeferred* from = nullptr;
 };
-hipError_t launch_gemm_ex(const GemmSegs& segs, const GemmRows& rows, void* ws, hipStream_t s);
+hipError_t launch_gemm_ex(const GemmSegs& segs, const GemmRows& rows, void* ws, hipStream_t s,
+                          GemmDeferred* defer_out = nullptr);
 
 // ---- vector kernels (k_vec.hip) ----
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t N, float eps, hipStream_t s);
