@@ -692,7 +692,8 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
         // The producer's partials lie beyond its own staged rows and scales;
         // in a shared workspace this launch's rows and scales must end at or
         // before those (a staged row no longer than the producer's).
-        if (from->T != T || from->M != N || (from->ws == ws && np > from->n_pad)) return hipErrorInvalidValue;
+        if (!from->y || from->T != T || from->M != N || (from->ws == ws && np > from->n_pad))
+            return hipErrorInvalidValue;
         xin.x = from->y;
         xin.part = from->part;
         xin.split = from->split;
@@ -726,7 +727,9 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     }
     e = launch(0, mtot, plan.bm);
     if (e != hipSuccess || a.split == 1) return e;
-    if (defer_out && nseg == 1 && (mtot & 3u) == 0) {
+    bool no_res = true;
+    for (int i = 0; i < nseg; ++i) no_res = no_res && sg.res[i] == nullptr;
+    if (defer_out && (nseg == 1 || no_res) && (mtot & 3u) == 0) {
         // the next GEMM's row conversion sums the partials
         defer_out->valid = true;
         defer_out->part = part;
@@ -735,7 +738,7 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
         defer_out->M = mtot;
         defer_out->meta = a.meta;
         defer_out->res = sg.res[0];
-        defer_out->y = sg.y[0];
+        defer_out->y = nseg == 1 ? sg.y[0] : nullptr;  // several matrices: the consumer knows the layout
         defer_out->ws = ws;
         defer_out->n_pad = np;
         return hipSuccess;

@@ -47,37 +47,65 @@ __device__ __forceinline__ float2 rope_pair(float2 x, float c, float sn) {
     return make_float2(a0 - b0, a1 + b1);
 }
 
+// Reduced Q|K|V pair (x0, x1) at column c of token t from the GEMM's split-K
+// partials: (sum_s part[s][t][c..c+1]) * pm.x, NaN where pm.y is set (the
+// order of k_gemm_reduce and gemm_store).
+__device__ __forceinline__ float2 part_pair(const float* part, uint32_t split, size_t plane, float2 pm, size_t at) {
+    float2 v = *reinterpret_cast<const float2*>(part + at);
+    for (uint32_t sp = 1; sp < split; ++sp) {
+        const float2 w = *reinterpret_cast<const float2*>(part + sp * plane + at);
+        v.x += w.x;
+        v.y += w.y;
+    }
+    v.x = v.x * pm.x;
+    v.y = v.y * pm.x;
+    if (pm.y != 0.0f) v = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+    return v;
+}
+
 __global__ __launch_bounds__(256) void k_rope_kv_rows(float* __restrict__ Q, const float* __restrict__ K,
                                                       const float* __restrict__ V, const float* __restrict__ ct,
                                                       const float* __restrict__ st, uint32_t pos0,
                                                       uint32_t n_heads, uint32_t n_kv, uint32_t max_seq,
-                                                      float* __restrict__ kv_layer) {
+                                                      float* __restrict__ kv_layer, const float* __restrict__ part,
+                                                      uint32_t split, const float2* __restrict__ pmeta, uint32_t T) {
     const uint32_t t = blockIdx.x, P = pos0 + t;
     const uint32_t qd = n_heads * kPHd, kvd = n_kv * kPHd;
     const float* c = ct + (size_t)P * kPHd;
     const float* sn = st + (size_t)P * kPHd;
     float* q = Q + (size_t)t * qd;
+    // reduction mode: the Q|K|V GEMM's partial row t, [q | k | v] columns
+    const uint32_t ld = qd + 2 * kvd;
+    const size_t plane = (size_t)T * ld, prow = (size_t)t * ld;
+    const float2 pm = part ? pmeta[t] : make_float2(1.0f, 0.0f);
     for (uint32_t p = threadIdx.x; p < qd / 2; p += 256) {
         const uint32_t i = 2 * p, e = i % kPHd;
         float2* qp = reinterpret_cast<float2*>(q + i);
-        *qp = rope_pair(*qp, c[e], sn[e]);
+        const float2 x = part ? part_pair(part, split, plane, pm, prow + i) : *qp;
+        *qp = rope_pair(x, c[e], sn[e]);
     }
     const float* k = K + (size_t)t * kvd;
     const float* v = V + (size_t)t * kvd;
     for (uint32_t p = threadIdx.x; p < kvd / 2; p += 256) {
         const uint32_t i = 2 * p, h = i / kPHd, e = i % kPHd;
         float* dst = kv_layer + ((size_t)h * max_seq + P) * 2 * kPHd;
-        *reinterpret_cast<float2*>(dst + e) = rope_pair(*reinterpret_cast<const float2*>(k + i), c[e], sn[e]);
-        *reinterpret_cast<float2*>(dst + kPHd + e) = *reinterpret_cast<const float2*>(v + i);
+        const float2 kx = part ? part_pair(part, split, plane, pm, prow + qd + i)
+                               : *reinterpret_cast<const float2*>(k + i);
+        const float2 vx = part ? part_pair(part, split, plane, pm, prow + qd + kvd + i)
+                               : *reinterpret_cast<const float2*>(v + i);
+        *reinterpret_cast<float2*>(dst + e) = rope_pair(kx, c[e], sn[e]);
+        *reinterpret_cast<float2*>(dst + kPHd + e) = vx;
     }
 }
 
 hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const float* cos_tab,
                                const float* sin_tab, uint32_t pos0, uint32_t T, uint32_t n_heads, uint32_t n_kv,
-                               uint32_t max_seq, float* kv_layer, hipStream_t s) {
-    if (T == 0 || n_kv == 0 || (uint64_t)pos0 + T > max_seq) return hipErrorInvalidValue;
+                               uint32_t max_seq, float* kv_layer, hipStream_t s, const float* part, uint32_t split,
+                               const float2* pmeta) {
+    if (T == 0 || n_kv == 0 || (uint64_t)pos0 + T > max_seq || (part && (split == 0 || !pmeta)))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_rope_kv_rows, dim3(T), dim3(256), 0, s, Q, K, V, cos_tab, sin_tab, pos0, n_heads, n_kv,
-                       max_seq, kv_layer);
+                       max_seq, kv_layer, part, split, pmeta, T);
     return hipGetLastError();
 }
 

@@ -421,9 +421,15 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         xn.T = T;
         xn.N = c.dim;
         xn.from = &pend;
-        QH_E(launch_gemm_ex(qkv, xn, p->pf_ws, s));
-        QH_E(launch_rope_kv_rows(p->pf_q, p->pf_k, p->pf_v, p->cos_tab, p->sin_tab, pos0, T, c.n_heads,
-                                 c.n_kv_heads, c.max_seq_len, kvl, s));
+        GemmDeferred qkv_part;  // the Q|K|V reduction is left to the RoPE pass
+        QH_E(launch_gemm_ex(qkv, xn, p->pf_ws, s, &qkv_part));
+        if (qkv_part.valid)
+            QH_E(launch_rope_kv_rows(p->pf_q, nullptr, nullptr, p->cos_tab, p->sin_tab, pos0, T, c.n_heads,
+                                     c.n_kv_heads, c.max_seq_len, kvl, s, qkv_part.part, qkv_part.split,
+                                     qkv_part.meta));
+        else
+            QH_E(launch_rope_kv_rows(p->pf_q, p->pf_k, p->pf_v, p->cos_tab, p->sin_tab, pos0, T, c.n_heads,
+                                     c.n_kv_heads, c.max_seq_len, kvl, s));
         PrefillAttnArgs aa;
         aa.q = p->pf_q;
         aa.kv = kvl;

@@ -101,10 +101,12 @@ struct GemmSegs {
     const float* res[3] = {};
     uint32_t M[3] = {};
 };
-// A one-matrix GEMM with a K split can leave its reduction to the next
-// GEMM's row conversion (launch_gemm_ex with defer_out): the partials, the
-// per-token scale and the residual are summed there in the reduction's own
-// order (bit-identical), the rows written to y, and then converted.  valid is
+// A GEMM with a K split can leave its reduction to the next kernel
+// (launch_gemm_ex with defer_out; one matrix, or several without
+// residuals): a one-matrix producer to the next GEMM's row conversion, where
+// the partials, the per-token scale and the residual are summed in the
+// reduction's own order (bit-identical), the rows written to y, and then
+// converted; the prefill's Q|K|V to the RoPE / KV-cache pass.  valid is
 // false when the launch had no split (y is then already written).
 struct GemmDeferred {
     bool valid = false;
@@ -112,7 +114,7 @@ struct GemmDeferred {
     uint32_t split = 0, T = 0, M = 0;
     const float2* meta = nullptr;  // the producer's per-token (2^-e, non-finite flag)
     const float* res = nullptr;    // its residual rows [T][M] (or null)
-    float* y = nullptr;            // its output rows [T][M]
+    float* y = nullptr;            // its output rows [T][M] (one matrix; else null)
     const void* ws = nullptr;      // its workspace and staged row length
     uint32_t n_pad = 0;
 };
