@@ -197,10 +197,13 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
     // scratch memory)
     typedef float stage_v __attribute__((ext_vector_type(4 * kLoads)));
     stage_v kr, vr;
-    using NoV = std::false_type;
-    using WithV = std::true_type;
-    auto fetch = [&](uint32_t st, auto with_vc) {
-        constexpr bool with_v = decltype(with_vc)::value;
+    // mode: 0 = K rows, 1 = K and V rows, 2 = V rows
+    using NoV = std::integral_constant<int, 0>;
+    using WithV = std::integral_constant<int, 1>;
+    using OnlyV = std::integral_constant<int, 2>;
+    auto fetch = [&](uint32_t st, auto modec) {
+        constexpr int mode = decltype(modec)::value;
+        constexpr bool with_k = mode != 2, with_v = mode != 0;
 #pragma unroll
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
@@ -208,11 +211,13 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
             uint32_t j = st * kAttnKS + r;
             j = j < n_keys ? j : n_keys - 1u;
             const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)j * 2 * kPHd) + c;
-            const float4 k4 = src[0];
-            kr[4 * u] = k4.x;
-            kr[4 * u + 1] = k4.y;
-            kr[4 * u + 2] = k4.z;
-            kr[4 * u + 3] = k4.w;
+            if constexpr (with_k) {
+                const float4 k4 = src[0];
+                kr[4 * u] = k4.x;
+                kr[4 * u + 1] = k4.y;
+                kr[4 * u + 2] = k4.z;
+                kr[4 * u + 3] = k4.w;
+            }
             if constexpr (with_v) {
                 const float4 v4 = src[kPHd / 4];
                 vr[4 * u] = v4.x;
@@ -222,13 +227,16 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
             }
         }
     };
-    auto put = [&](auto with_vc) {
-        constexpr bool with_v = decltype(with_vc)::value;
+    auto put = [&](auto modec) {
+        constexpr int mode = decltype(modec)::value;
+        constexpr bool with_k = mode != 2, with_v = mode != 0;
 #pragma unroll
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
-            *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) = make_float4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+            if constexpr (with_k)
+                *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) =
+                    make_float4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
             if constexpr (with_v)
                 *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) =
                     make_float4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
@@ -256,74 +264,127 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
         return d0 + d1;
     };
 
-    // ---- pass 1: row max (this half's keys, then both halves) ----
+    // Row max over the 16 keys of d (scores of keys jb .. jb+15).
     float mx = -INFINITY;
-    fetch(0, NoV{});
-    for (uint32_t st = 0; st < n_stages; ++st) {
-        __syncthreads();  // the previous stage's reads are done
-        put(NoV{});
-        __syncthreads();
-        if (st + 1 < n_stages) fetch(st + 1, NoV{});
+    auto max_sub = [&](uint32_t jb, const f4v& d) {
 #pragma unroll
-        for (uint32_t s2 = 0; s2 < 2; ++s2) {
-            const uint32_t sub = 2 * half + s2;
-            const uint32_t jb = st * kAttnKS + sub * 16;
-            if (jb >= n_keys) break;
-            const f4v d = scores(sub);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t j = jb + 4 * lg + r;
-                const float sc = d[r] * a.scale;
-                if (q_ok && j <= P) mx = fmaxf(mx, sc);
-            }
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t j = jb + 4 * lg + r;
+            const float sc = d[r] * a.scale;
+            if (q_ok && j <= P) mx = fmaxf(mx, sc);
         }
-    }
-    fetch(0, WithV{});  // pass 2's first block, in flight during the exchange
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (lane < 16) xmax[half][hw][lane] = mx;
-    __syncthreads();
-    mx = fmaxf(xmax[0][hw][li], xmax[1][hw][li]);
-
-    // ---- pass 2: e_j, their sum and P.V over this half's keys ----
+    };
+    // Both halves' maxima, through LDS.
+    auto exchange_max = [&]() {
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (lane < 16) xmax[half][hw][lane] = mx;
+        __syncthreads();
+        mx = fmaxf(xmax[0][hw][li], xmax[1][hw][li]);
+    };
+    // e_j of the 16 keys of d, their sum and P.V with the staged V rows.
     f4v acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     float sum = 0.0f;
-    for (uint32_t st = 0; st < n_stages; ++st) {
-        __syncthreads();
-        put(WithV{});
-        __syncthreads();
-        if (st + 1 < n_stages) fetch(st + 1, WithV{});
+    auto pv_sub = [&](uint32_t sub, uint32_t jb, const f4v& d) {
+        float e[4];
 #pragma unroll
-        for (uint32_t s2 = 0; s2 < 2; ++s2) {
-            const uint32_t sub = 2 * half + s2;
-            const uint32_t jb = st * kAttnKS + sub * 16;
-            if (jb >= n_keys) break;
-            const f4v d = scores(sub);
-            float e[4];
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t j = jb + 4 * lg + r;
+            const float dd = d[r] * a.scale - mx;
+            float ev = 0.0f;
+            if (q_ok && j <= P) ev = (j < Sv) ? exp_approx(dd) : expf(dd);
+            e[r] = ev;
+            sum += ev;
+        }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t j = jb + 4 * lg + r;
-                const float dd = d[r] * a.scale - mx;
-                float ev = 0.0f;
-                if (q_ok && j <= P) ev = (j < Sv) ? exp_approx(dd) : expf(dd);
-                e[r] = ev;
-                sum += ev;
+        for (int kk = 0; kk < 4; ++kk) {
+            const float* vr = &lkv[1][sub * 16 + 4 * lg + kk][0];
+            const float4 v0 = *reinterpret_cast<const float4*>(vr + 4 * li);
+            const float4 v1 = *reinterpret_cast<const float4*>(vr + 64 + 4 * li);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.x, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.y, acc[1], 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.z, acc[2], 0, 0, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.w, acc[3], 0, 0, 0);
+            acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.x, acc[4], 0, 0, 0);
+            acc[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.y, acc[5], 0, 0, 0);
+            acc[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.z, acc[6], 0, 0, 0);
+            acc[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.w, acc[7], 0, 0, 0);
+        }
+    };
+
+    constexpr uint32_t kCacheStages = 8;  // up to 512 keys: pass 1's scores stay in registers
+    if (n_stages <= kCacheStages) {
+        f4v sc[kCacheStages][2];
+        // ---- pass 1: scores and row max ----
+        fetch(0, NoV{});
+#pragma unroll
+        for (uint32_t st = 0; st < kCacheStages; ++st) {
+            if (st < n_stages) {
+                __syncthreads();  // the previous stage's reads are done
+                put(NoV{});
+                __syncthreads();
+                if (st + 1 < n_stages) fetch(st + 1, NoV{});
+#pragma unroll
+                for (uint32_t s2 = 0; s2 < 2; ++s2) {
+                    const uint32_t sub = 2 * half + s2;
+                    const uint32_t jb = st * kAttnKS + sub * 16;
+                    if (jb < n_keys) {
+                        sc[st][s2] = scores(sub);
+                        max_sub(jb, sc[st][s2]);
+                    }
+                }
             }
+        }
+        fetch(0, OnlyV{});  // pass 2's first block, in flight during the exchange
+        exchange_max();
+        // ---- pass 2: e_j, their sum and P.V (V rows only staged) ----
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const float* vr = &lkv[1][sub * 16 + 4 * lg + kk][0];
-                const float4 v0 = *reinterpret_cast<const float4*>(vr + 4 * li);
-                const float4 v1 = *reinterpret_cast<const float4*>(vr + 64 + 4 * li);
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.x, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.y, acc[1], 0, 0, 0);
-                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.z, acc[2], 0, 0, 0);
-                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.w, acc[3], 0, 0, 0);
-                acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.x, acc[4], 0, 0, 0);
-                acc[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.y, acc[5], 0, 0, 0);
-                acc[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.z, acc[6], 0, 0, 0);
-                acc[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.w, acc[7], 0, 0, 0);
+        for (uint32_t st = 0; st < kCacheStages; ++st) {
+            if (st < n_stages) {
+                __syncthreads();
+                put(OnlyV{});
+                __syncthreads();
+                if (st + 1 < n_stages) fetch(st + 1, OnlyV{});
+#pragma unroll
+                for (uint32_t s2 = 0; s2 < 2; ++s2) {
+                    const uint32_t sub = 2 * half + s2;
+                    const uint32_t jb = st * kAttnKS + sub * 16;
+                    if (jb < n_keys) pv_sub(sub, jb, sc[st][s2]);
+                }
+            }
+        }
+    } else {
+        // ---- pass 1: row max (this half's keys, then both halves) ----
+        fetch(0, NoV{});
+        for (uint32_t st = 0; st < n_stages; ++st) {
+            __syncthreads();  // the previous stage's reads are done
+            put(NoV{});
+            __syncthreads();
+            if (st + 1 < n_stages) fetch(st + 1, NoV{});
+#pragma unroll
+            for (uint32_t s2 = 0; s2 < 2; ++s2) {
+                const uint32_t sub = 2 * half + s2;
+                const uint32_t jb = st * kAttnKS + sub * 16;
+                if (jb >= n_keys) break;
+                max_sub(jb, scores(sub));
+            }
+        }
+        fetch(0, WithV{});  // pass 2's first block, in flight during the exchange
+        exchange_max();
+        // ---- pass 2: scores again (bit-identical), e_j, sum and P.V ----
+        for (uint32_t st = 0; st < n_stages; ++st) {
+            __syncthreads();
+            put(WithV{});
+            __syncthreads();
+            if (st + 1 < n_stages) fetch(st + 1, WithV{});
+#pragma unroll
+            for (uint32_t s2 = 0; s2 < 2; ++s2) {
+                const uint32_t sub = 2 * half + s2;
+                const uint32_t jb = st * kAttnKS + sub * 16;
+                if (jb >= n_keys) break;
+                pv_sub(sub, jb, scores(sub));
             }
         }
     }
