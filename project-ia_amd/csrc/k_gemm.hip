@@ -51,7 +51,7 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kBufFlagsG = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 constexpr int kKB = 2;                  // Q4_0 blocks per K-step
-constexpr int kInner = 8;               // blocks per inner sum
+constexpr int kInner = 16;              // blocks per inner sum
 constexpr int kXRow = 72;               // LDS halfs per staged X row (64 + 8 pad)
 
 // In-group order of the 8 elements a lane feeds to the MFMA: the nibble
