@@ -130,9 +130,16 @@ def test_gemv_config_shapes_vs_fp64_and_avx2(qa, name):
     y_avx2 = orc.gemv(W, M, N, x)
     mx, rms = stats(y, y64, cond)
     amx, arms = stats(y_avx2, y64, cond)
-    print(f"{name}: gpu max {mx:.3e} rms {rms:.3e} | avx2 max {amx:.3e} rms {arms:.3e}")
+    # the plain relative error, over the outputs whose magnitude is at least
+    # the median (outputs that cancel to ~0 have no meaningful plain error)
+    big = np.abs(y64) >= np.median(np.abs(y64))
+    plain = float(np.max(np.abs(y[big].astype(np.float64) - y64[big]) / np.abs(y64[big])))
+    aplain = float(np.max(np.abs(y_avx2[big].astype(np.float64) - y64[big]) / np.abs(y64[big])))
+    print(f"{name}: gpu max {mx:.3e} rms {rms:.3e} plain(>=median) {plain:.3e} | "
+          f"avx2 max {amx:.3e} rms {arms:.3e} plain(>=median) {aplain:.3e}")
     assert mx <= 1e-5
     assert mx <= amx and rms <= arms
+    assert plain <= 1e-5
 
 
 def test_gemv_lm_head_vs_fp64(qa):
