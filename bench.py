@@ -737,6 +737,57 @@ def summarize_traffic(fetch_dir, write_dir, cmd):
     print(json.dumps(res))
 
 
+# Decode attention at context 2048 (config 4, pos 2047 onward): algorithmic
+# bytes per dispatch of the three kernels, per layer (8 KV heads x 2048
+# positions x 128 floats of K or V; 32 query heads).  The cache rows hold K
+# and V side by side, so each kernel reads half of every 1-KB row.
+ATTN_KEYS, ATTN_HEADS, ATTN_KV, ATTN_HD = 2048, 32, 8, 128
+ATTN_CHUNKS_PV = (ATTN_KEYS + 255) // 256
+ATTN_ALG = {
+    # K rows + q, scores and 64-key chunk maxima written
+    "k_attn_scores": ATTN_KV * ATTN_KEYS * ATTN_HD * 4 + ATTN_HEADS * ATTN_HD * 4 + ATTN_HEADS * ATTN_KEYS * 4
+    + ATTN_HEADS * (ATTN_KEYS // 64) * 4,
+    # V rows + scores and chunk maxima read, P.V partials and chunk sums written
+    "k_attn_pv": ATTN_KV * ATTN_KEYS * ATTN_HD * 4 + ATTN_HEADS * ATTN_KEYS * 4 + ATTN_HEADS * (ATTN_KEYS // 64) * 4
+    + ATTN_CHUNKS_PV * ATTN_HEADS * ATTN_HD * 4 + ATTN_CHUNKS_PV * ATTN_HEADS * 4,
+    # partials and sums read, the 4096-float output's digit planes written
+    "k_attn_combine": ATTN_CHUNKS_PV * ATTN_HEADS * ATTN_HD * 4 + ATTN_CHUNKS_PV * ATTN_HEADS * 4 + 13 * 16 * 128,
+}
+
+
+def summarize_attn_traffic(fetch_dir, write_dir, cmd):
+    """profiles/attention_traffic.json: FETCH_SIZE and WRITE_SIZE per
+    dispatch of the decode-step attention kernels, from two --pmc passes
+    over the config-4 decode leg (median over every dispatch of a kernel),
+    scaled by the plain-copy calibration of profiles/gemv_traffic.json (the
+    same counters on the same part)."""
+    cal = json.loads((REPO / "profiles" / "gemv_traffic.json").read_text())["calibration"]
+    per = {k: {} for k in ATTN_ALG}
+    for cname, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = [r for r in _counter_rows(d) if r.get("Counter_Name") == cname]
+        for k in ATTN_ALG:
+            vals = [float(r["Counter_Value"]) for r in rows if ("qh::" + k + "<") in r["Kernel_Name"]
+                    or ("qh::" + k + "(") in r["Kernel_Name"]]
+            if not vals:
+                raise SystemExit(f"{cname}: no {k} dispatches under {d}")
+            g = float(np.median(vals))
+            per[k][cname] = {"dispatches": len(vals), "kib_per_dispatch": g,
+                             "bytes_per_dispatch": g * 1024.0 * cal[cname]["scale"]}
+    res = {"workload": "config-4 decode step, context 2048..2080 (the bench's decode leg), per layer",
+           "kernels": {k: {"alg_bytes_per_dispatch": ATTN_ALG[k],
+                           "traffic_bytes_per_dispatch": round(per[k]["FETCH_SIZE"]["bytes_per_dispatch"]
+                                                               + per[k]["WRITE_SIZE"]["bytes_per_dispatch"]),
+                           "traffic_over_alg": round((per[k]["FETCH_SIZE"]["bytes_per_dispatch"]
+                                                      + per[k]["WRITE_SIZE"]["bytes_per_dispatch"]) / ATTN_ALG[k], 4),
+                           "counters": per[k]} for k in ATTN_ALG},
+           "calibration": "profiles/gemv_traffic.json (FETCH_SIZE x%.4f, WRITE_SIZE x%.4f)"
+           % (cal["FETCH_SIZE"]["scale"], cal["WRITE_SIZE"]["scale"]),
+           "command": cmd}
+    p = REPO / "profiles" / "attention_traffic.json"
+    p.write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res))
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (profiles/gemv_traffic.json), or None."""
@@ -802,10 +853,15 @@ def main():
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/gemv_traffic.json from two --pmc output dirs")
+    ap.add_argument("--summarize-attn-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/attention_traffic.json from two --pmc passes over the decode leg")
     ap.add_argument("--traffic-cmd", default="", help="command line recorded with the summary")
     args = ap.parse_args()
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic, args.traffic_cmd)
+        return
+    if args.summarize_attn_traffic:
+        summarize_attn_traffic(*args.summarize_attn_traffic, args.traffic_cmd)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (batch-1 decode of an 8B model is not "
