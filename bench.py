@@ -285,7 +285,7 @@ def run_decode(args):
             m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
             m.upload_kv(kv)
             _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
-        prefill = None if args.no_prompt else run_prompt(m, h)
+        prefill = None if args.no_prompt else run_prompt(m, h, args.prompt_tokens)
         m.close()
         avg_ctx = DEC_POS + 1 + (steps - 1) / 2
         bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
@@ -302,7 +302,7 @@ def run_decode(args):
                "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
                                    "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
         if prefill is not None:
-            out["prefill_512"] = prefill
+            out["prefill_%d" % args.prompt_tokens] = prefill
         if not args.no_cpu:
             out["cpu_baseline"], out["first_token_matches_cpu"] = run_cpu_decode(path, kv, first_tok, int(toks[0]),
                                                                                 args.cpu_decode_tokens)
@@ -325,11 +325,14 @@ def prompt_flop(n_layers=32, T=PROMPT_T):
     return n_layers * (2 * T * w + attn) + 2 * v * d
 
 
-def run_prompt(m, h, reps=3):
-    """llama_forward of a 512-token prompt at position 0 on the 32-layer
-    model (the batched prefill), wall clock around the synchronous call."""
+def run_prompt(m, h, T=PROMPT_T, reps=3):
+    """llama_forward of a T-token prompt (512 by default) at position 0 on
+    the 32-layer model (the batched prefill, in chunks of up to 512 tokens),
+    wall clock around the synchronous call."""
+    if T < 1 or T > h.max_seq:
+        raise SystemExit(f"bench.py: --prompt-tokens must be 1..{h.max_seq}")
     rng = np.random.default_rng(2026)
-    toks = [int(t) for t in rng.integers(0, h.vocab, PROMPT_T)]
+    toks = [int(t) for t in rng.integers(0, h.vocab, T)]
     m.forward(toks, 0)  # first call allocates the prefill buffers
     times = []
     for _ in range(reps):
@@ -337,15 +340,15 @@ def run_prompt(m, h, reps=3):
         m.forward(toks, 0)
         times.append(time.perf_counter() - t0)
     ms = 1e3 * sum(times) / len(times)
-    fl = prompt_flop()
-    log(f"[bench] prompt: {PROMPT_T} tokens in {ms:.2f} ms ({PROMPT_T / ms * 1e3:.0f} tok/s)")
-    return {"tokens": PROMPT_T, "ms": round(ms, 3), "tok_s": round(PROMPT_T / ms * 1e3, 1), "reps": reps,
+    fl = prompt_flop(T=T)
+    log(f"[bench] prompt: {T} tokens in {ms:.2f} ms ({T / ms * 1e3:.0f} tok/s)")
+    return {"tokens": T, "ms": round(ms, 3), "tok_s": round(T / ms * 1e3, 1), "reps": reps,
             "useful_tflop_s": round(fl / (ms * 1e-3) / 1e12, 1),
             "frac_of_fp16_mfma_peak": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-            "workload": "llama_forward(512 tokens, pos 0) on the config-4 model (32 layers, Llama-3-8B shape, "
-                        "Q4_0): every projection an MFMA GEMM, causal fp32-MFMA attention, KV rows 0..511 "
+            "workload": "llama_forward(%d tokens, pos 0) on the config-4 model (32 layers, Llama-3-8B shape, "
+                        "Q4_0): every projection an MFMA GEMM, causal fp32-MFMA attention, KV rows 0..%d "
                         "written, LM head of the last token; wall clock of the synchronous call incl. the "
-                        "token upload and the 513 KB logits download"}
+                        "token upload and the 513 KB logits download" % (T, T - 1)}
 
 
 def run_cpu_decode(path, kv, first_tok, gpu_tok0, n_tokens):
@@ -848,7 +851,9 @@ def main():
     ap.add_argument("--no-sample", action="store_true", help="skip the q_sample_token leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill GEMM leg")
     ap.add_argument("--no-prompt", action="store_true",
-                    help="skip the 512-token llama_forward prompt on the config-4 model")
+                    help="skip the llama_forward prompt on the config-4 model")
+    ap.add_argument("--prompt-tokens", type=int, default=PROMPT_T,
+                    help="tokens of that prompt (default 512; up to the decode model's context)")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
