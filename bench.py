@@ -591,6 +591,9 @@ def run_prefill(args):
             "ms_per_step": round(ms_step, 4), "steps": steps, "tokens_per_s": round(T / (ms_step * 1e-3), 1),
             "useful_flop_per_step": PREFILL_FLOP, "TFLOP_s": round(tflops, 1),
             "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS,
+            # each useful product takes two MFMA products (x's fp16 hi and lo parts against the
+            # same exact weight operand), so the matrix cores run at twice the useful rate
+            "mfma_issue_util": round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "launch_us": {"gate_up": round(ms_gu * 1e3, 1), "down": round(ms_d * 1e3, 1)},
             "wall_s": round(wall, 3), "cpu_baseline": cpu}
 
