@@ -177,9 +177,14 @@ void q_free_memory(q_context* __restrict__ ctx) {
     }
 }
 
-// Reference src/core/utils.c:11-31.
+// Reference src/core/utils.c:11-31.  Callers pass any int (the reference's
+// own tests pass codes outside the enum); the code is read as an int, since
+// C++ gives an enum without a fixed type only its enumerators' range.
 const char* q_strerror(q_error_code err) {
-    switch (err) {
+    static_assert(sizeof(q_error_code) == sizeof(int), "q_error_code is passed as an int");
+    int code;
+    std::memcpy(&code, &err, sizeof code);
+    switch (code) {
         case Q_OK: return "Success";
         case Q_ERR_NULL_PTR: return "Null pointer argument";
         case Q_ERR_FILE_OPEN: return "Failed to open file";

@@ -2,12 +2,15 @@
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 PKG_DIR = Path(__file__).resolve().parent.parent  # project-ia_amd/
-LIB_PATH = PKG_DIR / "build" / "libqorus_hip.so"
+# QORUS_HIP_LIB selects another build of the same library (the host-sanitizer
+# build of `make -C project-ia_amd asan`, for the CPU tests of the host code).
+LIB_PATH = Path(os.environ.get("QORUS_HIP_LIB") or PKG_DIR / "build" / "libqorus_hip.so")
 
 Q_OK = 0
 Q_F32 = 0
