@@ -245,6 +245,50 @@ def test_load_errors(tmp_path):
         assert L.L.q_tokenizer_load(C.byref(L.t), None) == -10
 
 
+def test_load_fuzz_matches_oracle(tmp_path):
+    """Seeded corruptions of a valid tokenizer file (truncations, flipped
+    bytes, rewritten header words, zeroed or enlarged entry lengths): this
+    library's loader returns the oracle's code for every one and, where both
+    accept the file, encodes and decodes as the oracle does.  (Under the
+    host-sanitizer build this is also the loader's memory-safety check.)"""
+    rng = random.Random(2027)
+    v = [bytes([i]) if i else b"\x01" for i in range(256)] + [b"ab", b"<s>", b"</s>", b"<pad>"]
+    base = tmp_path / "base.bin"
+    otk.write(base, vocab=v, merges=[(97, 98, 256), (256, 256, 258), (104, 105, 259)], bos=257, eos=258, pad=259)
+    good = base.read_bytes()
+    L = Lib(qa.lib())
+    n_ok = 0
+    for k in range(300):
+        d = bytearray(good)
+        kind = k % 5
+        if kind == 0:
+            d = d[:rng.randrange(0, len(d))]
+        elif kind == 1:
+            for _ in range(rng.randint(1, 4)):
+                d[rng.randrange(len(d))] = rng.randrange(256)
+        elif kind == 2:
+            w = rng.choice([2, 3, 4, 5, 6, 7])  # vocab, merges, bos, eos, pad, reserved
+            d[4 * w:4 * w + 4] = rng.choice([0, 1, 5, 261, 262, 70000, 1000000, 1000001, 0xFFFFFFFF]).to_bytes(4, "little")
+        elif kind == 3:
+            d[32 + 2 * rng.randrange(200)] = rng.choice([0, 1, 2, 200, 255])
+        else:
+            i = rng.randrange(len(good) - 12, len(good) - 3)
+            d[i:i + 4] = rng.choice([96, 255, 259, 260, 261, 65536]).to_bytes(4, "little")
+        path = tmp_path / f"f{k}.bin"
+        path.write_bytes(bytes(d))
+        want_rc, ot = otk.load(path)
+        rc = L.load(path)
+        assert rc == want_rc, (k, kind, rc, want_rc)
+        if rc == 0:
+            n_ok += 1
+            for text in (b"abab hi", b"hhii", b"\x05\x06abab"):
+                assert L.encode(text, 16, True, True) == otk.encode(ot, text, 16, True, True), (k, text)
+            ids = [1, 97, 256, 258, 259, 260, 7]
+            assert L.decode(ids, 64) == otk.decode(ot, ids, 64), k
+            L.free()
+    assert 0 < n_ok < 300
+
+
 def test_python_front_end(tmp_path):
     path = tmp_path / "bytes.bin"
     qa.write_tokenizer(path, qa.byte_level_vocab(), merges=[(108, 108, 258)])
