@@ -113,7 +113,23 @@ __global__ __launch_bounds__(256) void k_gemm_xprep(const GemmXIn in, uint32_t T
                 const float4* p4 = reinterpret_cast<const float4*>(in.part + (size_t)t * N);
                 a = p4[2 * g];
                 b = p4[2 * g + 1];
-                for (uint32_t sp = 1; sp < in.split; ++sp) {
+                uint32_t sp = 1;
+                // 4 partials' loads in flight at a time; the sum stays
+                // sequential in split order
+                for (; sp + 4 <= in.split; sp += 4) {
+                    float4 c[4], d[4];
+#pragma unroll
+                    for (uint32_t u = 0; u < 4; ++u) {
+                        c[u] = p4[(sp + u) * pstride + 2 * g];
+                        d[u] = p4[(sp + u) * pstride + 2 * g + 1];
+                    }
+#pragma unroll
+                    for (uint32_t u = 0; u < 4; ++u) {
+                        a.x += c[u].x; a.y += c[u].y; a.z += c[u].z; a.w += c[u].w;
+                        b.x += d[u].x; b.y += d[u].y; b.z += d[u].z; b.w += d[u].w;
+                    }
+                }
+                for (; sp < in.split; ++sp) {
                     const float4 c = p4[sp * pstride + 2 * g], d = p4[sp * pstride + 2 * g + 1];
                     a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
                     b.x += d.x; b.y += d.y; b.z += d.z; b.w += d.w;
@@ -309,13 +325,15 @@ __device__ __forceinline__ h8v unpack8(uint32_t w) {
     return h8v{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-// MI: 16-row weight subtiles per wave (a wave's tile is 16*MI x 64).
-template <int WM, int WT, int MI>
+// MI: 16-row weight subtiles per wave, JT: 16-token subtiles per wave (a
+// wave's tile is 16*MI x 16*JT; JT < 4 for prompts of a few tokens, whose
+// single token tile would otherwise be mostly padding).
+template <int WM, int WT, int MI, int JT = 4>
 __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     constexpr int NT = 64 * WM * WT;
     constexpr int WR = 16 * MI;  // weight rows per wave
     constexpr int BM = WR * WM;
-    constexpr int BT = 64 * WT;
+    constexpr int BT = 16 * JT * WT;
     constexpr int XCH = 16 * BT / NT;                 // 16-byte X chunks per thread per K-step
     constexpr int WBL = (BM * kKB + NT - 1) / NT;     // weight blocks per thread per K-step
     constexpr bool kWAll = WBL * NT == BM * kKB;      // every thread stages WBL blocks
@@ -429,11 +447,11 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
 
-    f4v inner[MI][4], outer[MI][4];
+    f4v inner[MI][JT], outer[MI][JT];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < JT; ++j) {
             inner[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
             outer[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -473,8 +491,8 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
             // One token subtile at a time: its hi and lo parts, then the MI
             // weight subtiles.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 64 * wt + 16 * j + lr;
+            for (int j = 0; j < JT; ++j) {
+                const int t = 16 * JT * wt + 16 * j + lr;
                 const h8v Ah = *reinterpret_cast<const h8v*>(&lx[buf][0][t][32 * kb + 8 * lq]);
                 const h8v Al = *reinterpret_cast<const h8v*>(&lx[buf][1][t][32 * kb + 8 * lq]);
 #pragma unroll
@@ -491,7 +509,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < JT; ++j) {
                     outer[i][j] += inner[i][j];
                     inner[i][j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
                 }
@@ -510,8 +528,8 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     for (int i = 0; i < MI; ++i) {
         const uint32_t m = m0 + WR * wm + 16 * i + 4 * lq;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t t = t0 + 64 * wt + 16 * j + lr;
+        for (int j = 0; j < JT; ++j) {
+            const uint32_t t = t0 + 16 * JT * wt + 16 * j + lr;
             const f4v v = outer[i][j] + inner[i][j];
             if (m < M && t < a.T) {
                 if (a.split > 1) {
@@ -538,7 +556,16 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
         const uint32_t t = (uint32_t)(i / ld), c = (uint32_t)(i % ld);
         float v = a.part[i];
-        for (uint32_t sp = 1; sp < a.split; ++sp) v += a.part[(size_t)sp * n + i];
+        uint32_t sp = 1;
+        // 8 partials' loads in flight at a time; the sum stays sequential
+        for (; sp + 8 <= a.split; sp += 8) {
+            float w[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) w[u] = a.part[(size_t)(sp + u) * n + i];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) v += w[u];
+        }
+        for (; sp < a.split; ++sp) v += a.part[(size_t)sp * n + i];
         const uint32_t sg = seg_of_col(a, c);
         gemm_store(a, sg, t, c - a.part_off[sg], v);
     }
@@ -562,10 +589,18 @@ static uint32_t gemm_npad(uint32_t N) { return (N + 63u) & ~63u; }
 // on MI355X at T = 512: a launch takes rounds x (16 us + K-steps x 2.12 us
 // for 256-row tiles, 1.66 us for 192-row tiles), a round being up to 256
 // workgroups (one per CU); a reduction about 1 us plus its traffic at 5 TB/s.
+// Up to 128 tokens (one 128-token tile) the plan instead takes the smallest
+// token tile of 16, 32, 64 or 128 holding them (one wave per token tile
+// below 128, 16*JT tokens per wave) and the smallest K split (a power of
+// two, each split keeping kInner blocks) that gives at least 224 workgroups
+// (448 for the one-wave tiles, of which several fit a CU):
+// measured at 16-128 tokens on the Llama-3 shapes, within a few us of the
+// best tile and split, 1.2-3.4x faster than 128-token tiles at K split <= 8.
 struct GemmPlan {
     uint32_t bm;     // tile height of the (first) launch
     uint32_t split;
     uint32_t cut;    // the total row count: one launch
+    uint32_t bt;     // token tile: 128 (two waves of 64 tokens) or 64, 32, 16 (one wave)
 };
 
 static uint32_t gemm_rounds(uint32_t wgs) { return (wgs + 255u) / 256u; }
@@ -585,10 +620,24 @@ static GemmPlan gemm_plan(const uint32_t* Ms, int nseg, uint32_t T, uint32_t nbl
         }
         return n;
     };
+    if (T <= kGemmBT) {
+        const uint32_t bt = T <= 16u ? 16u : T <= 32u ? 32u : T <= 64u ? 64u : 128u;
+        const uint32_t wgs = tiles(0, mtot, 256u) * ((T + bt - 1) / bt);
+        uint32_t sp = 1;
+        // (each split keeps a whole inner sum of kInner blocks: with shorter
+        // splits the sequential sum of the partials can exceed the AVX2
+        // order's error at N = 4096)
+        // (the small tiles fit two or more workgroups per CU: 448 of them
+        // still run in one round)
+        const uint32_t target = bt == 128u ? 224u : 448u;
+        while (2 * sp <= max_split && wgs * sp < target && nblk >= 2 * sp * kInner) sp *= 2;
+        return GemmPlan{256u, sp, mtot, bt};
+    }
+    max_split = std::min(max_split, 8u);
     auto launch_us = [&](uint32_t wgs, uint32_t bm, uint32_t steps) {
         return gemm_rounds(wgs) * (16.0 + steps * (bm == 256u ? 2.12 : 1.66));
     };
-    GemmPlan best{256u, 1u, mtot};
+    GemmPlan best{256u, 1u, mtot, kGemmBT};
     double best_c = 1e30;
     for (uint32_t bm : {256u, 192u}) {
         for (uint32_t sp = 1; sp <= max_split; sp *= 2u) {
@@ -597,7 +646,7 @@ static GemmPlan gemm_plan(const uint32_t* Ms, int nseg, uint32_t T, uint32_t nbl
             if (sp > 1) c += 1.0 + (double)(sp + 1) * T * mtot * 4.0 / 5e6;
             if (c < best_c) {
                 best_c = c;
-                best = GemmPlan{bm, sp, mtot};
+                best = GemmPlan{bm, sp, mtot, kGemmBT};
             }
         }
     }
@@ -606,7 +655,7 @@ static GemmPlan gemm_plan(const uint32_t* Ms, int nseg, uint32_t T, uint32_t nbl
                          launch_us(tiles(r, mtot, 192u) * n_tt, 192u, steps_of(1));
         if (c < best_c) {
             best_c = c;
-            best = GemmPlan{256u, 1u, r};
+            best = GemmPlan{256u, 1u, r, kGemmBT};
         }
     }
     return best;
@@ -615,7 +664,7 @@ static GemmPlan gemm_plan(const uint32_t* Ms, int nseg, uint32_t T, uint32_t nbl
 // The K split a workspace is sized for: the plan of M_total rows as one
 // matrix (a launch over several matrices takes at most this split).
 static uint32_t gemm_ws_split(uint32_t M_total, uint32_t T, uint32_t nblk) {
-    return gemm_plan(&M_total, 1, T, nblk, 8u).split;
+    return gemm_plan(&M_total, 1, T, nblk, 32u).split;
 }
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -680,7 +729,7 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     a.nblk = N / 32;
     a.T = T;
     a.N_pad = np;
-    a.n_tt = tp / kGemmBT;
+    a.n_tt = (T + plan.bt - 1) / plan.bt;
     a.split = plan.split;
     a.blk_per_split = ((a.nblk + a.split - 1) / a.split + kKB - 1) / kKB * kKB;
     a.part = part;
@@ -714,7 +763,13 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
         gemm_rows_args(g, sg, r0, r1, bm, row_bytes);
         const uint32_t pairs = g.mt_end[g.nseg - 1] * g.split * g.n_tt;
         const uint32_t grid = g.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
-        if (bm == 256u)
+        if (plan.bt == 16u)
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 1>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
+        else if (plan.bt == 32u)
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 2>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
+        else if (plan.bt == 64u)
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 4>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
+        else if (bm == 256u)
             hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 4>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, g);
         else
             hipLaunchKernelGGL((k_gemm_q4<kGemmWM, kGemmWT, 3>), dim3(grid), dim3(64 * kGemmWM * kGemmWT), 0, s, g);

@@ -11,6 +11,8 @@
 // token-by-token result for every seq_len.)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cstdint>
 #include <type_traits>
 
@@ -52,7 +54,19 @@ __device__ __forceinline__ float2 rope_pair(float2 x, float c, float sn) {
 // order of k_gemm_reduce and gemm_store).
 __device__ __forceinline__ float2 part_pair(const float* part, uint32_t split, size_t plane, float2 pm, size_t at) {
     float2 v = *reinterpret_cast<const float2*>(part + at);
-    for (uint32_t sp = 1; sp < split; ++sp) {
+    uint32_t sp = 1;
+    // 8 loads in flight at a time; the sum stays sequential in split order
+    for (; sp + 8 <= split; sp += 8) {
+        float2 w[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const float2*>(part + (sp + u) * plane + at);
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            v.x += w[u].x;
+            v.y += w[u].y;
+        }
+    }
+    for (; sp < split; ++sp) {
         const float2 w = *reinterpret_cast<const float2*>(part + sp * plane + at);
         v.x += w.x;
         v.y += w.y;
@@ -78,7 +92,10 @@ __global__ __launch_bounds__(256) void k_rope_kv_rows(float* __restrict__ Q, con
     const uint32_t ld = qd + 2 * kvd;
     const size_t plane = (size_t)T * ld, prow = (size_t)t * ld;
     const float2 pm = part ? pmeta[t] : make_float2(1.0f, 0.0f);
-    for (uint32_t p = threadIdx.x; p < qd / 2; p += 256) {
+    // pairs are split over gridDim.y workgroups per token (more than one for
+    // short prompts, whose rows are few)
+    const uint32_t p0 = threadIdx.x + 256u * blockIdx.y, pstep = 256u * gridDim.y;
+    for (uint32_t p = p0; p < qd / 2; p += pstep) {
         const uint32_t i = 2 * p, e = i % kPHd;
         float2* qp = reinterpret_cast<float2*>(q + i);
         const float2 x = part ? part_pair(part, split, plane, pm, prow + i) : *qp;
@@ -86,7 +103,7 @@ __global__ __launch_bounds__(256) void k_rope_kv_rows(float* __restrict__ Q, con
     }
     const float* k = K + (size_t)t * kvd;
     const float* v = V + (size_t)t * kvd;
-    for (uint32_t p = threadIdx.x; p < kvd / 2; p += 256) {
+    for (uint32_t p = p0; p < kvd / 2; p += pstep) {
         const uint32_t i = 2 * p, h = i / kPHd, e = i % kPHd;
         float* dst = kv_layer + ((size_t)h * max_seq + P) * 2 * kPHd;
         const float2 kx = part ? part_pair(part, split, plane, pm, prow + qd + i)
@@ -104,8 +121,9 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
                                const float2* pmeta) {
     if (T == 0 || n_kv == 0 || (uint64_t)pos0 + T > max_seq || (part && (split == 0 || !pmeta)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rope_kv_rows, dim3(T), dim3(256), 0, s, Q, K, V, cos_tab, sin_tab, pos0, n_heads, n_kv,
-                       max_seq, kv_layer, part, split, pmeta, T);
+    const uint32_t per_token = std::max(1u, std::min(8u, 256u / T));  // workgroups per token row
+    hipLaunchKernelGGL(k_rope_kv_rows, dim3(T, per_token), dim3(256), 0, s, Q, K, V, cos_tab, sin_tab, pos0, n_heads,
+                       n_kv, max_seq, kv_layer, part, split, pmeta, T);
     return hipGetLastError();
 }
 

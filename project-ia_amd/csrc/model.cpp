@@ -478,9 +478,12 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         hn.u = p->pf_u;
         hn.T = T;
         hn.N = c.hidden_dim;
-        // the last layer's rows feed the LM head: reduced here
-        QH_E(launch_gemm_ex(wd, hn, p->pf_ws, s, l + 1 < c.n_layers ? &pend : nullptr));
-        if (l + 1 == c.n_layers) pend.valid = false;
+        // The last layer's rows feed the LM head: reduced here.  So are they
+        // when the next Q|K|V stages longer rows (dim > hidden_dim) than
+        // W_down did: its staging would overwrite the partials it reads.
+        const bool defer_down = l + 1 < c.n_layers && c.dim <= c.hidden_dim;
+        QH_E(launch_gemm_ex(wd, hn, p->pf_ws, s, defer_down ? &pend : nullptr));
+        if (!defer_down) pend.valid = false;
     }
     if (last) {
         // LM head of RMSNorm(last row), as in the decode step.

@@ -76,6 +76,10 @@ def check_rows(W, M, N, X, Y, tokens, slack=None):
     (1000, 2080, 130),   # odd block count (65), two token tiles
     (512, 14336, 40),    # down-projection width, split-K
     (40, 8192, 257),     # few rows, three token tiles (no XCD order)
+    (300, 4096, 16),     # 16-token tiles, K split
+    (1024, 4096, 20),    # 32-token tiles
+    (512, 14336, 64),    # 64-token tiles, a deep K split
+    (2048, 14336, 9),    # 16-token tiles, K split 16
 ])
 def test_gemm_vs_oracle(qa, M, N, T):
     rng = orc.rng_for(M * 7 + N, T)
