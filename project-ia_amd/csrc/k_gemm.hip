@@ -753,7 +753,10 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     const uint32_t per = (np / 8 + 255) / 256;
     auto xprep = per <= 2 ? k_gemm_xprep<2> : per <= 4 ? k_gemm_xprep<4> : per <= 8 ? k_gemm_xprep<8>
                                                                              : k_gemm_xprep<16>;
-    hipLaunchKernelGGL(xprep, dim3(tp), dim3(256), 0, s, xin, T, N, np, const_cast<_Float16*>(a.xh),
+    // the rows the token tiles read (zeros past T): all tp rows for the
+    // 128-token tile, fewer for the small ones
+    const uint32_t rows = std::min(tp, a.n_tt * plan.bt);
+    hipLaunchKernelGGL(xprep, dim3(rows), dim3(256), 0, s, xin, T, N, np, const_cast<_Float16*>(a.xh),
                        const_cast<_Float16*>(a.xl), const_cast<float2*>(a.meta));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
