@@ -120,6 +120,22 @@ def test_prefill_short_prompts(qa, tmp_path, T):
         m.close()
 
 
+@pytest.mark.parametrize("T", [5, 33, 100])
+def test_prefill_small_tiles_with_k_splits(qa, tmp_path, T):
+    """Widths with 32 and 64 blocks per row, so that prompts of 5, 33 and
+    100 tokens take the 16-, 64- and 128-token tiles with K splits of 2-4:
+    the split-K partials summed by the next row conversion (W_down's, with
+    dim <= hidden) and by the RoPE/KV pass (Q|K|V's)."""
+    h = qa.QorusHeader(vocab=500, dim=1024, hidden=2048, n_layers=2, n_heads=8, n_kv=2, max_seq=128)
+    m, blob, kv = build(qa, tmp_path, h, 70 + T, 0)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(70, T).integers(0, h.vocab, T)]
+        check_prompt(qa, m, h, kv, ref, toks, 0, f"T={T}")
+    finally:
+        m.close()
+
+
 def test_prefill_chunks_past_512_tokens(qa, tmp_path):
     """A 600-token prompt at position 3: a 512-token chunk, then 88 tokens
     whose queries attend the first chunk's keys from the cache."""
