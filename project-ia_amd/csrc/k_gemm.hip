@@ -52,7 +52,6 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 constexpr int kBufFlagsG = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 constexpr int kKB = 2;                  // Q4_0 blocks per K-step
 constexpr int kInner = 16;              // blocks per inner sum
-constexpr int kXRow = 72;               // LDS halfs per staged X row (64 + 8 pad)
 
 // In-group order of the 8 elements a lane feeds to the MFMA: the nibble
 // unpack below yields (e0,e4), (e1,e5), (e2,e6), (e3,e7) as half pairs, so
@@ -328,21 +327,28 @@ __device__ __forceinline__ h8v unpack8(uint32_t w) {
 // MI: 16-row weight subtiles per wave, JT: 16-token subtiles per wave (a
 // wave's tile is 16*MI x 16*JT; JT < 4 for prompts of a few tokens, whose
 // single token tile would otherwise be mostly padding).
-template <int WM, int WT, int MI, int JT = 4>
+template <int WM, int WT, int MI, int JT = 4, int KB = kKB>
 __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     constexpr int NT = 64 * WM * WT;
     constexpr int WR = 16 * MI;  // weight rows per wave
     constexpr int BM = WR * WM;
     constexpr int BT = 16 * JT * WT;
-    constexpr int XCH = 16 * BT / NT;                 // 16-byte X chunks per thread per K-step
-    constexpr int WBL = (BM * kKB + NT - 1) / NT;     // weight blocks per thread per K-step
-    constexpr bool kWAll = WBL * NT == BM * kKB;      // every thread stages WBL blocks
-    static_assert(XCH * NT == 16 * BT, "tile/thread mismatch");
-    static_assert(BM * kKB % 64 == 0, "weight staging threads come in whole waves");
+    constexpr int XCK = 4 * KB;                       // 16-byte X chunks per staged row and part
+    constexpr int XROW = 32 * KB + 8;                 // LDS halfs per staged X row (8 pad)
+    constexpr int XCH = 2 * XCK * BT / NT;            // 16-byte X chunks per thread per K-step
+    constexpr int WBL = (BM * KB + NT - 1) / NT;      // weight blocks per thread per K-step
+    constexpr bool kWAll = WBL * NT == BM * KB;       // every thread stages WBL blocks
+    static_assert(XCH * NT == 2 * XCK * BT, "tile/thread mismatch");
+    static_assert(BM * KB % 64 == 0, "weight staging threads come in whole waves");
+    static_assert(KB == 2 || KB == 4, "K-step of 2 or 4 blocks");
+    static_assert(kInner % KB == 0, "inner sums end on K-step boundaries");
+    // A row's blocks sit in its KB slots rotated by the row, so that the
+    // per-lane 16-byte reads of 8 consecutive rows cover all 32 banks.
+    constexpr int kSwz = KB == 2 ? 2 : 1;
 
-    __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BT][kXRow];
-    __shared__ __attribute__((aligned(16))) uint32_t lw[2][BM][kKB][4];
-    __shared__ __attribute__((aligned(16))) float ls[2][kKB][BM];
+    __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BT][XROW];
+    __shared__ __attribute__((aligned(16))) uint32_t lw[2][BM][KB][4];
+    __shared__ __attribute__((aligned(16))) float ls[2][KB][BM];
 
     // ---- tile of this workgroup ----
     const uint32_t n_mt = a.mt_end[a.nseg - 1] * a.split;  // (m-tile, split) pairs
@@ -367,7 +373,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     const uint32_t row_bytes = a.nblk * 20u;
     const uint32_t b_begin = sp * a.blk_per_split;
     const uint32_t b_end = min(a.nblk, b_begin + a.blk_per_split);
-    const uint32_t nsteps = b_end > b_begin ? (b_end - b_begin + kKB - 1) / kKB : 0u;
+    const uint32_t nsteps = b_end > b_begin ? (b_end - b_begin + KB - 1) / KB : 0u;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -392,23 +398,25 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < XCH; ++c) {
         const uint32_t idx = (uint32_t)(tid + NT * c);
-        const uint32_t part = idx / (8u * BT);
-        const uint32_t rem = idx % (8u * BT);
-        const uint32_t t = rem / 8u, ch = rem % 8u;
+        const uint32_t part = idx / (XCK * BT);
+        const uint32_t rem = idx % (XCK * BT);
+        const uint32_t t = rem / XCK, ch = rem % XCK;
         xsrc[c] = (part ? a.xl : a.xh) + (size_t)(t0 + t) * a.N_pad + 8u * ch;
     }
     auto load_x = [&](uint32_t step) {
-        const uint32_t k0 = (b_begin + step * kKB) * 32u;  // < N_pad - 63 by construction (N_pad % 64 == 0)
+        // < N_pad - (32 KB - 1): splits start on multiples of KB blocks and
+        // N_pad is a multiple of 128
+        const uint32_t k0 = (b_begin + step * KB) * 32u;
 #pragma unroll
         for (int c = 0; c < XCH; ++c) gx[c] = *reinterpret_cast<const u4v*>(xsrc[c] + k0);
     };
     auto load_w = [&](uint32_t step, auto setc) {
         constexpr int set = decltype(setc)::value;
-        const uint32_t b0 = b_begin + step * kKB;
+        const uint32_t b0 = b_begin + step * KB;
 #pragma unroll
         for (int j = 0; j < WBL; ++j) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
-            const uint32_t r = idx / kKB, kb = idx % kKB;
+            const uint32_t r = idx / KB, kb = idx % KB;
             const uint32_t b = b0 + kb;
             // rows >= M read zeros; threads past the tile's blocks (kWAll
             // false) load some row of the buffer and store nothing
@@ -422,24 +430,22 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
     // LDS buffer `buf` (also the weight register set) <- the staged step.
     auto store_step = [&](uint32_t step, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
-        const uint32_t b0 = b_begin + step * kKB;
+        const uint32_t b0 = b_begin + step * KB;
 #pragma unroll
         for (int c = 0; c < XCH; ++c) {
             const uint32_t idx = (uint32_t)(tid + NT * c);
-            const uint32_t part = idx / (8u * BT);
-            const uint32_t rem = idx % (8u * BT);
-            const uint32_t t = rem / 8u, ch = rem % 8u;
+            const uint32_t part = idx / (XCK * BT);
+            const uint32_t rem = idx % (XCK * BT);
+            const uint32_t t = rem / XCK, ch = rem % XCK;
             *reinterpret_cast<u4v*>(&lx[buf][part][t][8u * ch]) = gx[c];
         }
 #pragma unroll
         for (int j = 0; j < WBL; ++j) {
             const uint32_t idx = (uint32_t)(tid + NT * j);
-            const uint32_t r = idx / kKB, kb = idx % kKB;
-            if (kWAll || idx < (uint32_t)(BM * kKB)) {  // wave-uniform: BM * kKB is a multiple of 64
-                // the two blocks of a row swap slots in rows with bit 2 set, so
-                // the per-lane reads of 16 rows spread over all 32 banks
+            const uint32_t r = idx / KB, kb = idx % KB;
+            if (kWAll || idx < (uint32_t)(BM * KB)) {  // wave-uniform: BM * KB is a multiple of 64
                 // A zero scale removes a masked block: its products are finite.
-                *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> 2) & 1u)][0]) = gq[buf][j];
+                *reinterpret_cast<u4v*>(&lw[buf][r][kb ^ ((r >> kSwz) & (KB - 1u))][0]) = gq[buf][j];
                 ls[buf][kb][r] = b0 + kb < b_end ? gs[buf][j] : 0.0f;
             }
         }
@@ -475,7 +481,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
         load_x(min(step + 1, nsteps - 1));
         load_w(min(step + 2, nsteps - 1), bufc);  // set buf held step's weights, now in LDS
 #pragma unroll
-        for (int kb = 0; kb < kKB; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {
             // The weight fragment is the MFMA's A operand (D rows = weight
             // rows, D columns = tokens): register r of lane l holds weight row
             // 4*(l/16) + r of the subtile for token l%16, so each lane has 4
@@ -485,7 +491,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const int r = WR * wm + 16 * i + lr;
-                B[i] = unpack8(lw[buf][r][kb ^ ((r >> 2) & 1)][lq]);
+                B[i] = unpack8(lw[buf][r][kb ^ ((r >> kSwz) & (KB - 1))][lq]);
                 s[i] = *reinterpret_cast<const f4v*>(&ls[buf][kb][WR * wm + 16 * i + 4 * lq]);
             }
             // One token subtile at a time: its hi and lo parts, then the MI
@@ -504,7 +510,7 @@ __global__ __launch_bounds__(64 * WM * WT) void k_gemm_q4(const GemmArgs a) {
                 }
             }
         }
-        nb_in += kKB;
+        nb_in += KB;
         if (nb_in >= kInner) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
@@ -575,10 +581,14 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kGemmWM = 4, kGemmWT = 2;
+// K-step of the 16- and 32-token tiles: 4 blocks (80 contiguous bytes of
+// each weight row per step, half the steps and barriers; their X tile
+// leaves the LDS room)
+constexpr int kSmallKB = 4;
 constexpr uint32_t kGemmBT = 64 * kGemmWT;  // token rows per tile
 
 static uint32_t gemm_tpad(uint32_t T) { return (T + kGemmBT - 1) / kGemmBT * kGemmBT; }
-static uint32_t gemm_npad(uint32_t N) { return (N + 63u) & ~63u; }
+static uint32_t gemm_npad(uint32_t N) { return (N + 127u) & ~127u; }  // whole K-steps of up to 4 blocks
 
 // Launch plan of a GEMM over weight matrices of Ms[0..nseg) rows (each tiled
 // on its own), T tokens and nblk blocks per row: the tile height (256 or 192
@@ -731,7 +741,8 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
     a.N_pad = np;
     a.n_tt = (T + plan.bt - 1) / plan.bt;
     a.split = plan.split;
-    a.blk_per_split = ((a.nblk + a.split - 1) / a.split + kKB - 1) / kKB * kKB;
+    const uint32_t kb = plan.bt <= 32u ? (uint32_t)kSmallKB : (uint32_t)kKB;  // the kernel's K-step
+    a.blk_per_split = ((a.nblk + a.split - 1) / a.split + kb - 1) / kb * kb;
     a.part = part;
     a.part_ld = mtot;
     // The XCD-aware order needs the token-tile count to divide the 8 XCDs.
@@ -767,9 +778,9 @@ hipError_t launch_gemm_ex(const GemmSegs& sg, const GemmRows& in, void* ws, hipS
         const uint32_t pairs = g.mt_end[g.nseg - 1] * g.split * g.n_tt;
         const uint32_t grid = g.xcd_map ? (pairs + 7u) / 8u * 8u : pairs;
         if (plan.bt == 16u)
-            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 1>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 1, kSmallKB>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
         else if (plan.bt == 32u)
-            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 2>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
+            hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 2, kSmallKB>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
         else if (plan.bt == 64u)
             hipLaunchKernelGGL((k_gemm_q4<kGemmWM, 1, 4, 4>), dim3(grid), dim3(64 * kGemmWM), 0, s, g);
         else if (bm == 256u)
