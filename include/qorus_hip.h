@@ -75,13 +75,19 @@ size_t qh_gemv_workspace_bytes(uint32_t N);
  * is not 4-byte aligned.  `workspace` holds >= qh_gemv_workspace_bytes(N)
  * device bytes; NULL selects a library-owned per-device buffer (calls that
  * overlap on one device then race on it).  Result: within 1e-5 of the fp64
- * dot product relative to sum_j |W_ij x_j|.  x enters as integers with one
+ * dot product relative to sum_j |W_ij x_j| (an input that puts 7 or more
+ * outliers of similar size in a block, each meeting a zero weight, is
+ * outside this bound; see below).  x enters as integers with one
  * power-of-two scale per 32-element block (23-24 significant bits for the
- * block maximum); a block whose largest element carries more than 3/4 of
- * its magnitude sum (an activation outlier) gets a second 23-bit level, so
- * every element within 2^22 of its block maximum is exact.  Measured at the
- * Llama-3 shapes: 0.4-2e-8 with N(0,1) x, and the same with outliers of
- * 1e3..1e5 on zero weights, at or below the reference AVX2 order's error. */
+ * block maximum); a block where a few outliers set that scale (removing
+ * some 6 of its elements would leave less than 3/64 of its maximum) gets a
+ * second 23-bit level, so every element within 2^22 of its block maximum
+ * is exact.  Measured at the Llama-3 shapes: 0.4-2e-8 with N(0,1) x, and
+ * the same with 1..6 equal outliers of 1e3..1e5 per block, or mixed sizes,
+ * on zero weights, at or below the reference AVX2 order's error.  A block
+ * left on level 1 keeps at least 3/64 of its maximum outside any 6 of its
+ * elements; 8 equal outliers of 1e4 in every block on zero weights reach
+ * about 2e-5 (CPU emulation of the digits). */
 q_error_code qh_gemv_q4_f32(const q_tensor* W, const float* x, float* y, void* workspace,
                             qh_stream s);
 

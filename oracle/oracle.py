@@ -144,6 +144,8 @@ def lib():
         L = C.CDLL(str(_LIB))
         L.or_dequant_block.argtypes = [_u8p, _f32p]
         L.or_dequant_blocks.argtypes = [_u8p, C.c_uint64, _f32p]
+        L.or_set_threads.argtypes = [C.c_int]
+        L.or_set_threads.restype = None
         L.or_gemv_q4.argtypes = [_u8p, C.c_uint32, C.c_uint32, _f32p, _f32p]
         L.or_gemv_q4_rows.argtypes = [_u8p, C.c_uint32, C.c_uint32, C.c_uint32, _f32p, _f32p]
         L.or_gemv_q4_f64.argtypes = [_u8p, C.c_uint32, C.c_uint32, _f32p, _f64p, _f64p]
@@ -275,6 +277,12 @@ def ref():
 # ---------------------------------------------------------------------------
 # Oracle wrappers (numpy in, numpy out)
 # ---------------------------------------------------------------------------
+
+def set_threads(n: int) -> None:
+    """Threads for the oracle's GEMV rows and attention heads (1 by
+    default; any count gives the same bits)."""
+    lib().or_set_threads(int(n))
+
 
 def f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)

@@ -137,10 +137,19 @@ static void gemv_row(const uint8_t* row, uint32_t nblk, const float* x, float* y
     *y = hsum8(sl);
 }
 
+/* Threads for the row loops of the GEMV and the heads of the attention (1 by
+ * default).  Each row / head is computed by one thread in the order above,
+ * so the results are the same bits for any count; more threads only make
+ * long oracle runs (deep models, 512-token prompts) finish sooner. */
+static int g_threads = 1;
+
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+
 void or_gemv_q4_rows(const uint8_t* W, uint32_t r0, uint32_t r1, uint32_t N,
                      const float* x, float* y) {
     const uint32_t nblk = N / 32;
     const size_t row_bytes = (size_t)nblk * 20;
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && r1 - r0 >= 256)
     for (uint32_t i = r0; i < r1; i++) gemv_row(W + (size_t)i * row_bytes, nblk, x, &y[i]);
 }
 
@@ -531,26 +540,30 @@ void or_attention_decode(const float* q, const float* kv_layer, float* out,
                          uint32_t max_seq, uint32_t pos) {
     const uint32_t S = pos + 1;
     const float scale = 1.0f / sqrtf((float)head_dim);
-    float* sc = (float*)malloc((size_t)S * sizeof(float));
-    float* vt = (float*)malloc((size_t)S * sizeof(float));
     const size_t pos_stride = 2 * (size_t)head_dim;
     const size_t head_stride = (size_t)max_seq * pos_stride;
-    for (uint32_t h = 0; h < n_heads; h++) {
-        const uint32_t kvh = h / (n_heads / n_kv_heads);
-        const float* base = kv_layer + (size_t)kvh * head_stride;
-        const float* qh = q + (size_t)h * head_dim;
-        for (uint32_t j = 0; j < S; j++) {
-            const float d = or_dot_f32(qh, base + (size_t)j * pos_stride, head_dim);
-            sc[j] = d * scale;
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
+    {
+        float* sc = (float*)malloc((size_t)S * sizeof(float));
+        float* vt = (float*)malloc((size_t)S * sizeof(float));
+#pragma omp for schedule(static)
+        for (uint32_t h = 0; h < n_heads; h++) {
+            const uint32_t kvh = h / (n_heads / n_kv_heads);
+            const float* base = kv_layer + (size_t)kvh * head_stride;
+            const float* qh = q + (size_t)h * head_dim;
+            for (uint32_t j = 0; j < S; j++) {
+                const float d = or_dot_f32(qh, base + (size_t)j * pos_stride, head_dim);
+                sc[j] = d * scale;
+            }
+            or_softmax(sc, sc, S);
+            for (uint32_t d = 0; d < head_dim; d++) {
+                for (uint32_t j = 0; j < S; j++) vt[j] = base[(size_t)j * pos_stride + head_dim + d];
+                out[(size_t)h * head_dim + d] = or_dot_f32(sc, vt, S);
+            }
         }
-        or_softmax(sc, sc, S);
-        for (uint32_t d = 0; d < head_dim; d++) {
-            for (uint32_t j = 0; j < S; j++) vt[j] = base[(size_t)j * pos_stride + head_dim + d];
-            out[(size_t)h * head_dim + d] = or_dot_f32(sc, vt, S);
-        }
+        free(sc);
+        free(vt);
     }
-    free(sc);
-    free(vt);
 }
 
 /* ------------------------------------------------------------------------ */

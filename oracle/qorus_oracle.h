@@ -28,6 +28,10 @@ extern "C" {
 void or_dequant_block(const uint8_t* blk, float out[32]);
 void or_dequant_blocks(const uint8_t* blks, uint64_t n_blocks, float* out);
 
+/* Threads used by the GEMV row loops and the attention heads (default 1;
+ * results are the same bits for any count). */
+void or_set_threads(int n);
+
 /* GEMV in the reference AVX2 accumulation order; W is M x N, N % 32 == 0. */
 void or_gemv_q4(const uint8_t* W, uint32_t M, uint32_t N, const float* x, float* y);
 /* Same, rows [r0, r1) only (y indexed by absolute row). */

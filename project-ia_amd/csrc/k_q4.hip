@@ -21,17 +21,22 @@
 //    load covers 1280 contiguous bytes of a row.
 //  * Partial sums are reduced across the wave by butterflies and across
 //    waves through LDS in a fixed order (deterministic).
-// Outliers: a block whose largest element carries more than 3/4 of the
-// block's magnitude (an activation outlier) also gets a second level of
-// digits for the residual x*2^k - x_int, so every element within 2^22 of
-// the block maximum is represented exactly (qh_digits.hpp); the GEMV adds
-// that level's dot, one plane at a time, only in waves whose columns hold
-// such a block (found at the barrier that publishes the digits, or with
-// the digits themselves), in a loop of its own without prefetch so the
-// level-1 loop keeps its registers and occupancy.
+// Outliers: a block where a few activation outliers set the step (removing
+// some 6 of its elements would leave less than 3/64 of its maximum; the
+// exact rule is in qh_digits.hpp) also gets a second level of digits for
+// the residual x*2^k - x_int, so every element within 2^22 of the block
+// maximum is represented exactly; the GEMV adds that level's dot, one plane
+// at a time, only in waves whose columns hold such a block (found at the
+// barrier that publishes the digits, or with the digits themselves), in a
+// loop of its own without prefetch so the level-1 loop keeps its registers
+// and occupancy.
 // Accuracy (fp64-referenced, relative to sum_j |W_ij x_j|): 0.4-2e-8 at the
 // Llama-3 shapes with N(0,1) inputs, at or below the reference AVX2 order's,
-// and the same with outliers of 1e3..1e5 meeting zero weights (tested).
+// and the same with 1..6 outliers of 1e3..1e5 per block (and mixed sizes)
+// meeting zero weights, in one block or in every block (tested).  A block
+// left on level 1 keeps at least 3/64 of its maximum outside any 6 of its
+// elements; more zero-weighted outliers than that per block (7 or more of
+// similar size, next to values 1e3 times smaller) are outside the bound.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>

@@ -21,17 +21,23 @@ namespace qh {
 //    A_e) * 2^23) in 6 more planes.  A + 2^-23 B holds every element within
 //    2^22 of the block maximum exactly.  The planes of a block that is not
 //    wide are left unwritten; consumers read level 2 only through the flag.
-// A block is wide when its largest element carries more than three
-// quarters of the block's magnitude, 4 max|A| > 3 sum|A|: an activation
-// outlier, which on level 1 alone would leave the block's other elements
-// only the bits below its own (a 1e3 outlier among N(0,1) values carries
-// 97 %).  Ordinary distributions, heavy-tailed ones included, stay on
-// level 1, whose step is then below 2^-18 of the block's mean magnitude.
-// The test is on exact integers, so every producer below sets the same flag.
+// A block is wide unless, whichever 6 of its elements are removed, the rest
+// keep a magnitude sum of at least 3/64 of the block maximum (level-1
+// units).  Otherwise a few activation outliers set the step, and where they
+// meet zero weights the remaining elements keep only the bits below the
+// outliers' own.  The test takes lower bounds of that remainder that need
+// no sort: for any threshold t, (sum of all but the 6 largest |A_e|) >=
+// sum_e min(|A_e|, t) - 6 t, here at t1 = max|A| / 16 and t2 = max|A| / 64
+// (the larger bound decides).  So a block holding up to 6 outliers is wide
+// whenever its other elements sum to less than 3/64 of them: 1..6 outliers
+// of 1e3 or more among N(0,1) values always are.  N(0,1) inputs never
+// flag; heavy-tailed ones rarely (SwiGLU products of N(0, 8^2) gates and
+// ups: 3e-4 of their blocks; Student t3: 8e-6).  The sums are of exact
+// integers, so every producer below sets the same flag.
 // Layout: uint4 xd[13][pad]: planes 0..5, the meta word, planes 7..12.
 //
 // prep_lane: 32 consecutive lanes own one block (lane = element); block max,
-// NaN/Inf flag and the level-1 magnitude sum by cross-lane reductions, then
+// NaN/Inf flag and the clamped level-1 magnitude sums by cross-lane reductions, then
 // the digits and the 8-lane OR that packs each plane dword.  Lanes 0..5 of
 // each 8-lane group store the dwords of plane q (and of plane 7 + q for a
 // wide block), lanes 6..7 of the first two groups store the meta word.
@@ -42,7 +48,12 @@ constexpr uint32_t kXdMeta = 6;            // plane index of (k, z, wide, 0)
 constexpr uint32_t kXdLo = 7;              // first level-2 plane
 constexpr float kLoInv = 1.1920928955078125e-07f;  // 2^-23, the weight of level 2
 
-__device__ __forceinline__ bool block_wide(int amax, int asum) { return 4 * amax > 3 * asum; }
+// The wide test on c1 = sum_e min(|A_e|, amax >> 4) and c2 = sum_e
+// min(|A_e|, amax >> 6): both bounds of the remainder below 3 (amax >> 6).
+__device__ __forceinline__ bool block_wide(int amax, int c1, int c2) {
+    const int t1 = amax >> 4, t2 = amax >> 6;
+    return c1 - 6 * t1 < 3 * t2 && c2 - 6 * t2 < 3 * t2;
+}
 
 // Cross-lane steps on the DPP datapath (full-rate VALU, no LDS round trip):
 // quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2), and
@@ -99,9 +110,11 @@ __device__ inline void prep_lane(float v, uint32_t c, bool store, uint32_t pad, 
     const float t = bad ? 0.0f : ldexpf(v, k);
     const float ar = rintf(t);
     const int xi = (int)ar;
-    const int asum = half_sum_i(xi < 0 ? -xi : xi);
     const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
-    const bool wide = !bad && block_wide(amax, asum);
+    const int ax = xi < 0 ? -xi : xi;
+    const int c1 = half_sum_i(min(ax, amax >> 4));
+    const int c2 = half_sum_i(min(ax, amax >> 6));
+    const bool wide = !bad && block_wide(amax, c1, c2);
     const int sh = 4 * (e & 7);
     const int q = e & 7, i = e >> 3;
     // Packs one 6-digit value per lane into plane dwords (8-lane OR) and
@@ -191,23 +204,26 @@ __device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[13
     const bool bad = mb >= 0xFF000000u;
     float m;
     const int k = block_k(mb, bad, m);
+    const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
+    const int t1 = amax >> 4, t2 = amax >> 6;
     uint32_t pl[6][4];
-    int asum = 0;
+    int c1 = 0, c2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint32_t u[8], p8[6];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int a = bad ? 0 : (int)rintf(ldexpf(v[8 * i + e], k));
-            asum += a < 0 ? -a : a;
+            const int ax = a < 0 ? -a : a;
+            c1 += min(ax, t1);
+            c2 += min(ax, t2);
             u[e] = (uint32_t)(a + (int)kDigitBias);
         }
         planes8(u, p8);
 #pragma unroll
         for (int p = 0; p < 6; ++p) pl[p][i] = p8[p];
     }
-    const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
-    const bool wide = !bad && block_wide(amax, asum);
+    const bool wide = !bad && block_wide(amax, c1, c2);
 #pragma unroll
     for (int p = 0; p < 6; ++p) out[p] = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
     out[kXdMeta] = make_uint4((uint32_t)k, __float_as_uint(bad ? __builtin_nanf("") : 0.0f), (uint32_t)wide, 0u);
@@ -238,7 +254,7 @@ __device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[13
 // prep_block split over the 4 lanes of an aligned lane quad: lane i of the
 // quad holds elements 8i..8i+7 of the block in v and gets dword i of every
 // level-1 plane (pl, already XORed with 0x88888888) and the block's meta
-// words (k, z, wide).  The block maximum and magnitude sum are combined
+// words (k, z, wide).  The block maximum and clamped magnitude sums are combined
 // across the quad, so all 4 lanes must call it together; the digits are
 // those of prep_block bit for bit.  prep_quarter_lo gives the same lane's
 // dwords of the level-2 planes of a wide block.
@@ -251,20 +267,24 @@ __device__ __forceinline__ void prep_quarter(const float (&v)[8], uint32_t (&pl)
     const bool bad = mb >= 0xFF000000u;
     float m;
     const int k = block_k(mb, bad, m);
+    const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
+    const int t1 = amax >> 4, t2 = amax >> 6;
     uint32_t u[8];
-    int asum = 0;
+    int c1 = 0, c2 = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int a = bad ? 0 : (int)rintf(ldexpf(v[e], k));
-        asum += a < 0 ? -a : a;
+        const int ax = a < 0 ? -a : a;
+        c1 += min(ax, t1);
+        c2 += min(ax, t2);
         u[e] = (uint32_t)(a + (int)kDigitBias);
     }
     planes8(u, pl);
-    asum = quad_sum_i(asum);
-    const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
+    c1 = quad_sum_i(c1);
+    c2 = quad_sum_i(c2);
     k_out = (uint32_t)k;
     z_out = __float_as_uint(bad ? __builtin_nanf("") : 0.0f);
-    wide_out = (uint32_t)(!bad && block_wide(amax, asum));
+    wide_out = (uint32_t)(!bad && block_wide(amax, c1, c2));
 }
 
 __device__ __forceinline__ void prep_quarter_lo(const float (&v)[8], int k, uint32_t (&pl2)[6]) {

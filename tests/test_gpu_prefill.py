@@ -216,3 +216,46 @@ def test_causal_mask_entry_points(qa):
     d = qa.DeviceBuffer(64)
     assert lib.qh_causal_mask_f32(d.ptr, 4, 3, -1.0, None) == -15
     assert lib.qh_causal_mask_f32(d.ptr, 16, 16, -1.0, None) == -10  # 1 KB of rows, a 64-byte buffer
+
+
+def test_prefill_512_tokens_config4_widths(qa, tmp_path):
+    """The launch plan the bench's 512-token prompt times, checked: config-4
+    widths (d 4096, GQA 32/8 x 128, FFN 14336) with 2 layers and the
+    vocabulary cut to 1024, a 512-token prompt at position 0 (Q|K|V split-K
+    2, the 256/192-row cut of W_gate|W_up, W_down split 4, register-held
+    scores for 512 keys at GQA group 4), against the oracle's 511 cache
+    fills and last step (spread over host threads; the same bits as one).
+    W_gate's block scales are divided by 4 (gates of std ~2 instead of ~8):
+    the reference's SiLU jumps at g = -10 (its polynomial exp is 91.4 for
+    5 < x <= 10 and 22026 above), so a gate within a few ulp of -10 takes
+    either side in two correct fp32 orders and moves h_i by ~0.1 |u_i|;
+    with the generator's scales 38 of the prompt's 7.3 M layer-0 gates lie
+    within 1e-4 of it, and the tokens holding them differed from the oracle
+    by up to 1.3e-4 in the next layer's cache rows."""
+    import os
+    h = qa.QorusHeader(vocab=1024, dim=4096, hidden=14336, n_layers=2, n_heads=32, n_kv=8, max_seq=520)
+    path = tmp_path / "c4w.qorus"
+    qa.synthetic.write_synthetic_model(path, h, 73)
+    blob = np.fromfile(path, dtype=np.uint8)
+    lay = qa.model_layout(h)
+    for l in range(h.n_layers):
+        o = lay[f"{l}.w_gate"]
+        g = blob[o: o + h.hidden * (h.dim // 32) * 20].reshape(-1, 20)
+        g[:, 16:] = (g[:, 16:].copy().view(np.float32) * np.float32(0.25)).view(np.uint8)
+    blob.tofile(path)
+    m = qa.Model(path)
+    kv = np.zeros((h.n_layers, h.n_kv, h.max_seq, 2, 128), np.float32)
+    m.upload_kv(kv)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in orc.rng_for(73, 3).integers(0, h.vocab, 512)]
+        tok = check_prompt(qa, m, h, kv, ref, toks, 0, "512 tokens, config-4 widths")
+        # a decode step after the prompt reads the 512 prefilled rows
+        lg = m.forward([tok], 512)
+        tok_ref, lg_ref = ref.step(tok, 512)
+        assert rel_err(lg, lg_ref) <= 1e-4
+        assert int(np.argmax(lg)) == tok_ref
+    finally:
+        orc.set_threads(1)
+        m.close()

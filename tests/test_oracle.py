@@ -448,3 +448,32 @@ def test_decode_fp64_comparison_catches_planted_mistakes(tmp_path, mistake):
     tok64, logits64 = ref64.step(37, 13, mistake=mistake)
     scale = float(np.max(np.abs(logits64)))
     assert tok != tok64 or float(np.max(np.abs(logits.astype(np.float64) - logits64))) > 1e-4 * scale
+
+
+def test_oracle_threads_give_the_same_bits(tmp_path):
+    """or_set_threads only spreads GEMV rows and attention heads over
+    threads (each computed whole by one thread): the GEMV and a decode step
+    return the same bits with 1 and 8 threads."""
+    from qorus_amd.model_file import QorusHeader
+    from qorus_amd.synthetic import write_synthetic_model
+    rng = orc.rng_for(72)
+    W = orc.gen_q4(1000, 2048, rng)
+    x = orc.gen_f32(2048, rng)
+    h = QorusHeader(vocab=600, dim=512, hidden=768, n_layers=2, n_heads=8, n_kv=2, max_seq=64)
+    path = tmp_path / "thr.qorus"
+    write_synthetic_model(path, h, 72)
+    blob = np.fromfile(path, dtype=np.uint8)
+    out = []
+    try:
+        for n in (1, 8):
+            orc.set_threads(n)
+            kv = _kv_for(h, 40, 72)
+            tok, logits = orc.DecodeOracle(blob, kv).step(5, 40)
+            out.append((orc.gemv(W, 1000, 2048, x), tok, logits, kv))
+    finally:
+        orc.set_threads(1)
+    (y1, t1, l1, k1), (y8, t8, l8, k8) = out
+    assert np.array_equal(y1.view(np.uint32), y8.view(np.uint32))
+    assert t1 == t8
+    assert np.array_equal(l1.view(np.uint32), l8.view(np.uint32))
+    assert np.array_equal(k1.view(np.uint32), k8.view(np.uint32))
