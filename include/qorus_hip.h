@@ -171,12 +171,14 @@ q_error_code qh_silu_f32(const float* x, float* output, uint32_t N, qh_stream s)
 /* silu(gate) * up, the SwiGLU product of reference model.c:1516-1549. */
 q_error_code qh_silu_mul_f32(const float* gate, const float* up, float* output, uint32_t N,
                              qh_stream s);
-/* Reference src/ops/avx2/softmax.c:17-132 (sum reduced as a fixed tree);
- * x may alias output.  For N >= 16384 the work is spread over many
- * workgroups whose partial results live in a workspace: qh_softmax_f32
- * uses one library workspace per process (calls that may overlap on
- * different streams must use qh_softmax_f32_ws with a workspace of
- * qh_softmax_workspace_bytes(N) device bytes each). */
+/* Reference src/ops/avx2/softmax.c:17-132 in its summation order (eight
+ * lane sums over the first N&~7 elements, their fixed tree, then the tail
+ * in index order, times 1/sum): bit-exact with q_softmax_f32_avx2 where the
+ * tail's libm expf agrees with the device's (always when N % 8 == 0).
+ * x may alias output.  The partial results live in a workspace:
+ * qh_softmax_f32 uses one library workspace per process (calls that may
+ * overlap on different streams must use qh_softmax_f32_ws with a workspace
+ * of qh_softmax_workspace_bytes(N) device bytes each). */
 q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream s);
 size_t qh_softmax_workspace_bytes(uint32_t N);
 q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* workspace, qh_stream s);
@@ -191,7 +193,10 @@ q_error_code qh_argmax_f32_ws(const float* x, uint32_t N, uint32_t* index_out, v
 /* Softmax of x into output and the greedy argmax of x into *index_out in
  * one pass structure (no reference counterpart: the reference's LM-head
  * step runs q_softmax_f32_avx2 and the argmax of src/main.c:870-881 one
- * after the other; results are those two calls').  workspace holds
+ * after the other).  The index is the reference's; the softmax sums as a
+ * tree over many workgroups, so the probabilities match the reference's
+ * within 2e-6 relative (same zero pattern), not to the bit: the
+ * exact-order qh_softmax_f32 runs its lane sums in one wave.  workspace holds
  * qh_softmax_workspace_bytes(N) device bytes; x must not alias output
  * (Q_ERR_ALIASING). */
 q_error_code qh_softmax_argmax_f32_ws(const float* x, float* output, uint32_t N, uint32_t* index_out,
@@ -199,7 +204,8 @@ q_error_code qh_softmax_argmax_f32_ws(const float* x, float* output, uint32_t N,
 
 /* LM head + softmax + greedy argmax: logits = W . x (as qh_gemv_q4_f32),
  * probs = softmax(logits) and *index_out = argmax(logits) (as
- * qh_softmax_argmax_f32_ws: the same bits and index).  For 2048 < N <= 4096
+ * qh_softmax_argmax_f32_ws: the same bits and index; the probabilities are
+ * its tree-sum form).  For 2048 < N <= 4096
  * and M >= 16384 the GEMV also leaves the argmax's per-workgroup partials,
  * so no separate pass re-reads the logits (3 launches).  workspace holds
  * qh_gemv_softmax_workspace_bytes(M) device bytes; probs must not alias

@@ -36,24 +36,13 @@ q_error_code validate_gemv(const q_tensor* W, const float* x, const float* y) {
     return Q_OK;
 }
 
-// Library-owned GEMV workspace for device calls that pass none.
-static std::mutex g_ws_mu;
-static void* g_ws = nullptr;
-static size_t g_ws_bytes = 0;
-
-static q_error_code default_workspace(size_t bytes, void** out) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (g_ws_bytes < bytes) {
-        if (g_ws) {
-            QH_TRY(hipDeviceSynchronize());
-            QH_TRY(hipFree(g_ws));
-            g_ws = nullptr;
-            g_ws_bytes = 0;
-        }
-        QH_TRY(hipMalloc(&g_ws, bytes));
-        g_ws_bytes = bytes;
-    }
-    *out = g_ws;
+// The library's GEMV digit workspace (allocated once with the device state)
+// for device calls that pass none: inputs up to kLibGemvMaxN wide.  Calls
+// that overlap on one device share it and race.
+static q_error_code library_workspace(Device* d, uint32_t N, void** out) {
+    if (N > kLibGemvMaxN)
+        return fail_code(Q_ERR_INVALID_SIZE, "GEMV input wider than the library workspace: pass a workspace");
+    *out = d->gemv_ws;
     return Q_OK;
 }
 
@@ -89,8 +78,7 @@ q_error_code qh_gemv_q4_f32(const q_tensor* W, const float* x, float* y, void* w
     QH_TRY_CODE(validate_gemv(W, x, y));
     Device* d;
     QH_TRY_CODE(device(&d));
-    if (!workspace && needs_workspace(W->ne[1]))
-        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    if (!workspace && needs_workspace(W->ne[1])) QH_TRY_CODE(library_workspace(d, W->ne[1], &workspace));
     return gemv_device(W, W->data, x, nullptr, y, workspace, (hipStream_t)s);
 }
 
@@ -100,8 +88,7 @@ q_error_code qh_gemv_q4_f32_add(const q_tensor* W, const float* x, const float* 
     if (!residual) return Q_ERR_INVALID_ARG;
     Device* d;
     QH_TRY_CODE(device(&d));
-    if (!workspace && needs_workspace(W->ne[1]))
-        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(W->ne[1]), &workspace));
+    if (!workspace && needs_workspace(W->ne[1])) QH_TRY_CODE(library_workspace(d, W->ne[1], &workspace));
     return gemv_device(W, W->data, x, residual, y, workspace, (hipStream_t)s);
 }
 
@@ -154,7 +141,7 @@ q_error_code qh_gemv_q4_f32_multi(const q_tensor* const* Ws, const float* const*
     const uint32_t N = Ws[0]->ne[1];
     Device* d;
     QH_TRY_CODE(device(&d));
-    if (!workspace && needs_workspace(N)) QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(N), &workspace));
+    if (!workspace && needs_workspace(N)) QH_TRY_CODE(library_workspace(d, N, &workspace));
     QH_TRY(launch_gemv_f32(segs, (int)n, N, x, static_cast<uint4*>(workspace), (hipStream_t)s));
     return Q_OK;
 }
@@ -172,11 +159,25 @@ size_t gemv_softmax_ws_bytes(uint32_t M) {
 }
 
 q_error_code validate_gemv_softmax(const q_tensor* W, const float* x, const float* logits, const float* probs,
-                                   const uint32_t* index_out) {
+                                   const uint32_t* index_out, bool need_ws, const void* workspace) {
     QH_TRY_CODE(validate_gemv(W, x, logits));
-    if (!probs || !index_out) return Q_ERR_INVALID_ARG;
+    if (!probs || !index_out || (need_ws && !workspace)) return Q_ERR_INVALID_ARG;
     if (!aligned(probs, 32)) return Q_ERR_MISALIGNED;
     if (probs == logits || probs == x) return Q_ERR_ALIASING;
+    return Q_OK;
+}
+
+q_error_code check_gemv_softmax_memory(const q_tensor* W, const float* x, const float* logits, const float* probs,
+                                       const uint32_t* index_out, const void* workspace) {
+    // Every operand must be device memory covering what the kernels touch:
+    // a host or stale pointer becomes an error code, not a GPU fault.
+    const uint32_t M = W->ne[0], N = W->ne[1];
+    if (!device_range(W->data, (size_t)M * W->nb[0]) || !device_range(x, (size_t)N * 4) ||
+        !device_range(logits, (size_t)M * 4) || !device_range(probs, (size_t)M * 4) ||
+        !device_range(index_out, 4) || (workspace && !device_range(workspace, gemv_softmax_ws_bytes(M))))
+        return fail(hipErrorInvalidValue,
+                    "LM head: W->data, x, logits, probs, index_out or the workspace is not device memory of the "
+                    "required size");
     return Q_OK;
 }
 
@@ -199,7 +200,9 @@ q_error_code gemv_softmax_argmax_run(const q_tensor* W, const float* x, float* l
     void* gws = nullptr;
     if (needs_workspace(N)) {
         if (!may_allocate) return fail(hipErrorInvalidValue, "input wider than the in-kernel digit conversion");
-        QH_TRY_CODE(default_workspace(qh_gemv_workspace_bytes(N), &gws));
+        Device* d;
+        QH_TRY_CODE(device(&d));
+        QH_TRY_CODE(library_workspace(d, N, &gws));
     }
     QH_TRY(launch_gemv_f32(&seg, 1, N, x, static_cast<uint4*>(gws), st));
     QH_TRY(launch_softmax_argmax_ws(logits, probs, M, ws, index_out, st));
@@ -214,10 +217,10 @@ size_t qh_gemv_softmax_workspace_bytes(uint32_t M) { return gemv_softmax_ws_byte
 
 q_error_code qh_gemv_q4_f32_softmax_argmax(const q_tensor* W, const float* x, float* logits, float* probs,
                                            uint32_t* index_out, void* workspace, qh_stream s) {
-    QH_TRY_CODE(validate_gemv_softmax(W, x, logits, probs, index_out));
-    if (!workspace) return Q_ERR_INVALID_ARG;
+    QH_TRY_CODE(validate_gemv_softmax(W, x, logits, probs, index_out, true, workspace));
     Device* d;
     QH_TRY_CODE(device(&d));
+    QH_TRY_CODE(check_gemv_softmax_memory(W, x, logits, probs, index_out, workspace));
     return gemv_softmax_argmax_run(W, x, logits, probs, index_out, workspace, true, (hipStream_t)s);
 }
 

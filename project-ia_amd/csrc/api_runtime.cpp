@@ -8,6 +8,7 @@
 #include <mutex>
 #include <string>
 
+#include "qh_kernels.hpp"
 #include "qh_runtime.hpp"
 
 namespace qh {
@@ -47,6 +48,8 @@ q_error_code device(Device** out) {
         d->id = id;
         QH_TRY(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
         QH_TRY(hipMalloc(reinterpret_cast<void**>(&d->reduce_ws), kReduceWsBytes));
+        QH_TRY(hipMalloc(&d->gemv_ws, xd_bytes(kLibGemvMaxN / 32)));
+        QH_TRY_CODE(noalloc_scratch_init(id));
         g_dev = d;
     }
     *out = g_dev;

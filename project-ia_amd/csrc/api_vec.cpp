@@ -265,10 +265,12 @@ q_error_code q_softmax_f32_avx2(const float* __restrict__ x, float* __restrict__
     QH_TRY_CODE(device(&d));
     std::lock_guard<std::mutex> lk(d->mu);
     Stager st;
-    QH_TRY_CODE(st.open(d, Stager::round((size_t)N * 4)));
+    const size_t wsb = softmax_exact_ws_bytes(N);
+    QH_TRY_CODE(st.open(d, Stager::round((size_t)N * 4) + Stager::round(wsb)));
     float* dx = st.take(N);
+    float* ws = st.take((wsb + 3) / 4);
     QH_TRY_CODE(st.put(dx, x, N));
-    QH_TRY(launch_softmax_ws(dx, dx, N, d->reduce_ws, d->stream));
+    QH_TRY(launch_softmax_exact(dx, dx, N, ws, wsb, d->stream));
     return st.get(output, dx, N);
 }
 
@@ -321,11 +323,14 @@ q_error_code qh_softmax_f32(const float* x, float* output, uint32_t N, qh_stream
     QH_TRY_CODE(validate_softmax(x, output, N));
     Device* d;
     QH_TRY_CODE(device(&d));
-    QH_TRY(launch_softmax_ws(x, output, N, d->reduce_ws, (hipStream_t)s));
+    QH_TRY(launch_softmax_exact(x, output, N, d->reduce_ws, kReduceWsBytes, (hipStream_t)s));
     return Q_OK;
 }
 
-size_t qh_softmax_workspace_bytes(uint32_t N) { return softmax_workspace_bytes(N); }
+size_t qh_softmax_workspace_bytes(uint32_t N) {
+    const size_t a = softmax_workspace_bytes(N), b = softmax_exact_ws_bytes(N);
+    return a > b ? a : b;
+}
 size_t qh_argmax_workspace_bytes(uint32_t N) { return argmax_workspace_bytes(N); }
 
 q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* workspace, qh_stream s) {
@@ -333,7 +338,7 @@ q_error_code qh_softmax_f32_ws(const float* x, float* output, uint32_t N, void* 
     if (!workspace) return Q_ERR_INVALID_ARG;
     Device* d;
     QH_TRY_CODE(device(&d));
-    QH_TRY(launch_softmax_ws(x, output, N, static_cast<float*>(workspace), (hipStream_t)s));
+    QH_TRY(launch_softmax_exact(x, output, N, workspace, softmax_exact_ws_bytes(N), (hipStream_t)s));
     return Q_OK;
 }
 

@@ -374,25 +374,41 @@ __global__ __launch_bounds__(64 * W * G) void k_gemv_p(const GemvArgs a) {
             }
             uint32_t* ldw = reinterpret_cast<uint32_t*>(lds);
             bool wide_here = false;
+            uint32_t kqs[kQPass > 0 ? kQPass : 1];
+            int amq[kQPass > 0 ? kQPass : 1];
+            bool mq[kQPass > 0 ? kQPass : 1];
+            bool any_maybe = false;
 #pragma unroll
             for (int ps = 0; ps < kQPass; ++ps) {
                 const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
                 const uint32_t c = t >> 2, qi = t & 3u;
-                uint32_t pl[6], kq, zq, wq;
-                prep_quarter(xv[ps], pl, kq, zq, wq);  // whole quads share c, so they agree on c < kMaxBlk
+                uint32_t pl[6], zq;
+                prep_quarter(xv[ps], pl, kqs[ps], zq, amq[ps], mq[ps]);  // whole quads share c, so they agree on c < kMaxBlk
+                any_maybe |= mq[ps];
                 if (c < (uint32_t)kMaxBlk) {
 #pragma unroll
                     for (int p = 0; p < 6; ++p) ldw[((uint32_t)p * kMaxBlk + c) * 4u + qi] = pl[p];
-                    ldw[(kXdMeta * kMaxBlk + c) * 4u + qi] = qi == 0 ? kq : (qi == 1 ? zq : (qi == 2 ? wq : 0u));
+                    ldw[(kXdMeta * kMaxBlk + c) * 4u + qi] = qi == 0 ? kqs[ps] : (qi == 1 ? zq : 0u);
                 }
-                // Level 2 of a wide block (the others' stay unwritten: their
-                // readers go by the wide flag).
-                if (wq && c < (uint32_t)kMaxBlk) {
-                    uint32_t pl2[6];
-                    prep_quarter_lo(xv[ps], (int)kq, pl2);
+            }
+            // Second stage of the wide test, only where a block passed the
+            // first (the whole wave takes part: quad sums): the wide word
+            // and level 2 of a wide block (the others' level 2 stays
+            // unwritten: their readers go by the wide flag).
+            if (__ballot(any_maybe) != 0ull) {
 #pragma unroll
-                    for (int p = 0; p < 6; ++p) ldw[((kXdLo + (uint32_t)p) * kMaxBlk + c) * 4u + qi] = pl2[p];
-                    wide_here = true;
+                for (int ps = 0; ps < kQPass; ++ps) {
+                    const uint32_t t = (uint32_t)(ps * kThreads) + threadIdx.x;
+                    const uint32_t c = t >> 2, qi = t & 3u;
+                    const bool wq = quarter_wide(xv[ps], (int)kqs[ps], amq[ps], mq[ps]);
+                    if (wq && c < (uint32_t)kMaxBlk) {
+                        if (qi == 2) ldw[(kXdMeta * kMaxBlk + c) * 4u + qi] = 1u;
+                        uint32_t pl2[6];
+                        prep_quarter_lo(xv[ps], (int)kqs[ps], pl2);
+#pragma unroll
+                        for (int p = 0; p < 6; ++p) ldw[((kXdLo + (uint32_t)p) * kMaxBlk + c) * 4u + qi] = pl2[p];
+                        wide_here = true;
+                    }
                 }
             }
             // The barrier that publishes the digits also publishes each

@@ -92,9 +92,9 @@ __global__ void k_softmax_small(const float* __restrict__ x, uint32_t V, float* 
 constexpr uint32_t kMaxSlice = 4096;
 
 __global__ __launch_bounds__(kThreads) void k_max_part(const float* __restrict__ x, uint32_t V, Temp tp,
-                                                     float* __restrict__ part) {
+                                                     float* __restrict__ part, uint32_t slice) {
     __shared__ float red[kThreads / 64];
-    const uint32_t b0 = blockIdx.x * kMaxSlice, b1 = b0 + kMaxSlice < V ? b0 + kMaxSlice : V;
+    const uint32_t b0 = blockIdx.x * slice, b1 = V - b0 > slice ? b0 + slice : V;
     float m = -INFINITY;
     for (uint32_t i = b0 + threadIdx.x; i < b1; i += kThreads) m = fmaxf(m, temp_of(tp, x, i));
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -124,9 +124,9 @@ __global__ __launch_bounds__(kThreads) void k_exp_elems(const float* __restrict_
 // most kSparseTerms): only the nonzero terms are added, each to its lane's
 // sum in index order.  Adding a zero to a sum that starts at +0 never
 // changes it, so this is the dense sum to the bit.
-// Dense form: blocks of 512 elements (64 groups of 8) are staged through
-// LDS, the next block's global loads issued before the current block is
-// summed.
+// Dense form (more terms, or no list: nzl == nullptr): blocks of 512
+// elements (64 groups of 8) are staged through LDS, the next block's global
+// loads issued before the current block is summed.
 constexpr uint32_t kSparseTerms = 4096;
 
 __global__ __launch_bounds__(64) void k_lane_sums(const float* __restrict__ e, uint32_t V,
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(64) void k_lane_sums(const float* __restrict__ e, u
     __shared__ float blk[2][512];
     const uint32_t lane = threadIdx.x;
     const uint32_t nv = V & ~7u, ng = nv / 8;  // groups of 8 in the vector part
-    const uint32_t nz = nzc[0];
+    const uint32_t nz = nzl ? nzc[0] : 0xFFFFFFFFu;
     if (nz <= kSparseTerms) {
         float acc = 0.0f;
         for (uint32_t b = 0; b < nz; b += 64) {
@@ -295,9 +295,11 @@ __global__ __launch_bounds__(kThreads) void k_scan_chunks(uint32_t* __restrict__
     }
 }
 
+// Entries at offsets >= cap are not written (a caller that only reads the
+// list when it holds at most cap entries sizes it to cap).
 __global__ __launch_bounds__(kThreads) void k_scatter(const float* __restrict__ p, const uint8_t* __restrict__ m,
                                                     uint32_t V, const uint32_t* __restrict__ cc,
-                                                    uint32_t* __restrict__ list) {
+                                                    uint32_t* __restrict__ list, uint32_t cap) {
     const uint32_t chunk = blockIdx.x;
     const uint32_t i0 = chunk * kChunk + 4 * threadIdx.x;
     uint32_t bits, last1 = 0;
@@ -306,7 +308,17 @@ __global__ __launch_bounds__(kThreads) void k_scatter(const float* __restrict__ 
     uint32_t at = cc[chunk] + block_excl(c, &total);
 #pragma unroll
     for (uint32_t u = 0; u < 4; ++u)
-        if (bits & (1u << u)) list[at++] = i0 + u;
+        if (bits & (1u << u)) {
+            if (at < cap) list[at] = i0 + u;
+            ++at;
+        }
+}
+
+// y_i = e_i * inv[0] (the softmax's last step, N >= 8).
+__global__ __launch_bounds__(kThreads) void k_scale_inv(float* __restrict__ y, uint32_t N,
+                                                      const float* __restrict__ inv) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < N) y[i] = y[i] * inv[0];
 }
 
 // Selection and draw, one workgroup (steps 3-5).  The nonzero p, in index
@@ -644,13 +656,13 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
         fa.cand_n = nullptr;
     } else {
         const uint32_t G = (V + kMaxSlice - 1) / kMaxSlice;
-        QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, logits, V, tp, smx);
+        QH_K(k_max_part, dim3(G), dim3(kThreads), 0, s, logits, V, tp, smx, kMaxSlice);
         QH_K(k_exp_elems, grid, dim3(kThreads), 0, s, logits, V, tp, smx, G, probs);
         const uint32_t nch = (V + kChunk - 1) / kChunk;
         uint32_t* nzc = reinterpret_cast<uint32_t*>(scal + 8);
         QH_K(k_count, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, nch);
         QH_K(k_scan_chunks, dim3(1), dim3(kThreads), 0, s, chunks, nch, nzc);
-        QH_K(k_scatter, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, list);
+        QH_K(k_scatter, dim3(nch), dim3(kThreads), 0, s, probs, (const uint8_t*)nullptr, V, chunks, list, V);
         QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, probs, V, (const uint32_t*)list, (const uint32_t*)nzc, scal + 6);
         fa.inv = scal + 6;  // the filter scales the exponentials as it reads them
         fa.cand = list;
@@ -669,6 +681,82 @@ hipError_t launch_sample(const float* logits, const SampleParams& sp, void* ws, 
     fa.gvalid = W + L.gvalid;
     fa.token = token;
     QH_K(k_filter_draw, dim3(1), dim3(kSelThreads), 0, s, fa);
+#undef QH_K
+    return hipSuccess;
+}
+
+// ---------------------------------------------------------------------------
+// Softmax in q_softmax_f32_avx2's exact order (reference src/ops/avx2/
+// softmax.c:17-132): the sampler's steps 2 without a temperature.  N < 8:
+// the one-workgroup kernel's scalar path (libm-style expf, sequential sum,
+// e / sum).  N >= 8: slice maxima, e_i = exp_approx(x_i - m) below N & ~7
+// and expf above (written to y), the nonzero e_i listed in index order
+// when the workspace holds the list, the eight lane sums and tree of
+// k_lane_sums (sparse over the list when it holds at most kSparseTerms
+// entries, dense otherwise), then y_i *= 1 / sum.
+// Workspace: [parts: G floats][scal: 16 words][chunk counts: 2 nch words]
+// [list: min(N, kSparseTerms) words]; without room for the last two the
+// sums run dense.
+namespace {
+
+struct SmxExactLayout {
+    uint32_t slice, G, nch;
+    size_t parts, scal, chunks, list, full, dense;
+};
+
+// Slices of kMaxSlice elements, doubled until there are at most 1024.
+SmxExactLayout smx_exact_layout(uint32_t N) {
+    SmxExactLayout L;
+    L.slice = kMaxSlice;
+    while ((N + (uint64_t)L.slice - 1) / L.slice > 1024u) L.slice *= 2;
+    L.G = (uint32_t)((N + (uint64_t)L.slice - 1) / L.slice);
+    L.nch = (N + kChunk - 1) / kChunk;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    L.parts = 0;
+    L.scal = al((size_t)L.G * 4);
+    L.chunks = L.scal + 256;
+    L.dense = L.chunks;
+    L.list = L.chunks + al((size_t)2 * L.nch * 4);
+    L.full = L.list + al((size_t)(N < kSparseTerms ? N : kSparseTerms) * 4);
+    return L;
+}
+
+}  // namespace
+
+size_t softmax_exact_ws_bytes(uint32_t N) { return N < 8 ? 0 : smx_exact_layout(N).full; }
+
+hipError_t launch_softmax_exact(const float* x, float* y, uint32_t N, void* ws, size_t ws_bytes, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    if (N < 8) return launch_softmax(x, y, N, s);
+    const SmxExactLayout L = smx_exact_layout(N);
+    if (!ws || ws_bytes < L.dense) return hipErrorInvalidValue;
+    uint8_t* W = static_cast<uint8_t*>(ws);
+    float* parts = reinterpret_cast<float*>(W + L.parts);
+    float* scal = reinterpret_cast<float*>(W + L.scal);  // [0] count, [1] last, [8] 1/sum
+    const bool listed = ws_bytes >= L.full;
+    const Temp tp{N, 1.0f, 1.0f};  // x * 1.0f: the logits unchanged
+    const dim3 grid((N + kThreads - 1) / kThreads);
+    hipError_t e;
+#define QH_K(...)                                            \
+    do {                                                     \
+        hipLaunchKernelGGL(__VA_ARGS__);                     \
+        if ((e = hipGetLastError()) != hipSuccess) return e; \
+    } while (0)
+    QH_K(k_max_part, dim3(L.G), dim3(kThreads), 0, s, x, N, tp, parts, L.slice);
+    QH_K(k_exp_elems, grid, dim3(kThreads), 0, s, x, N, tp, (const float*)parts, L.G, y);
+    uint32_t* nzc = reinterpret_cast<uint32_t*>(scal);
+    const uint32_t* list = nullptr;
+    if (listed) {
+        uint32_t* chunks = reinterpret_cast<uint32_t*>(W + L.chunks);
+        uint32_t* lst = reinterpret_cast<uint32_t*>(W + L.list);
+        QH_K(k_count, dim3(L.nch), dim3(kThreads), 0, s, (const float*)y, (const uint8_t*)nullptr, N, chunks, L.nch);
+        QH_K(k_scan_chunks, dim3(1), dim3(kThreads), 0, s, chunks, L.nch, nzc);
+        QH_K(k_scatter, dim3(L.nch), dim3(kThreads), 0, s, (const float*)y, (const uint8_t*)nullptr, N,
+             (const uint32_t*)chunks, lst, kSparseTerms);
+        list = lst;
+    }
+    QH_K(k_lane_sums, dim3(1), dim3(64), 0, s, (const float*)y, N, list, (const uint32_t*)nzc, scal + 8);
+    QH_K(k_scale_inv, grid, dim3(kThreads), 0, s, y, N, (const float*)(scal + 8));
 #undef QH_K
     return hipSuccess;
 }

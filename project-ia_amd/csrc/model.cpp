@@ -549,6 +549,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     // heads, d_model up to 16384 (the Q|K|V epilogue's persistent GEMV).
     if (h->version < 3 || h->hidden_dim == 0 || h->max_seq_len == 0) return Q_ERR_INVALID_CONFIG;
     if (h->dim / 32 > kGemvF32MaxBlk) return Q_ERR_INVALID_CONFIG;
+    if (h->hidden_dim > 32768) return Q_ERR_INVALID_CONFIG;  // the prefill GEMM converts rows of N <= 32768
     const uint32_t group = h->n_kv_heads ? h->n_heads / h->n_kv_heads : 0;
     if (group != 1 && group != 2 && group != 4 && group != 8) return Q_ERR_INVALID_CONFIG;  // GQA groups built
     if (h->n_heads % h->n_kv_heads != 0 || h->dim % h->n_heads != 0 || h->dim / h->n_heads != 128)
@@ -745,6 +746,20 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     if (e == hipSuccess) e = hipMemcpy(p->sin_tab, sn, tab * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         fail(e, "decode plan upload");
+        plan_destroy(st);
+        return Q_ERR_ALLOC_FAILED;
+    }
+    // Everything a later call needs is allocated here, so no llama_forward
+    // (one token or a prompt) and no device generation loop allocates: the
+    // prefill rows and GEMM workspace for chunks of up to 512 tokens and the
+    // sampler's workspace.
+    q_error_code rc = prefill_alloc(p);
+    if (rc == Q_OK) {
+        const size_t wb = sample_workspace_bytes(cfg.vocab_size);
+        e = wb ? hipMalloc(&p->sample_ws, wb) : hipErrorInvalidValue;
+        if (e != hipSuccess) rc = fail(e, "sampler workspace");
+    }
+    if (rc != Q_OK) {
         plan_destroy(st);
         return Q_ERR_ALLOC_FAILED;
     }

@@ -27,8 +27,10 @@ namespace qh {
 // meet zero weights the remaining elements keep only the bits below the
 // outliers' own.  The test takes lower bounds of that remainder that need
 // no sort: for any threshold t, (sum of all but the 6 largest |A_e|) >=
-// sum_e min(|A_e|, t) - 6 t, here at t1 = max|A| / 16 and t2 = max|A| / 64
-// (the larger bound decides).  So a block holding up to 6 outliers is wide
+// sum_e min(|A_e|, t) - 6 t, here at t = max|A| (the plain magnitude sum,
+// which settles ordinary blocks; the clamped sums are then skipped), then
+// max|A| / 16 and max|A| / 64 (the block is wide when all three bounds
+// fall below 3/64 of max|A|).  So a block holding up to 6 outliers is wide
 // whenever its other elements sum to less than 3/64 of them: 1..6 outliers
 // of 1e3 or more among N(0,1) values always are.  N(0,1) inputs never
 // flag; heavy-tailed ones rarely (SwiGLU products of N(0, 8^2) gates and
@@ -48,8 +50,11 @@ constexpr uint32_t kXdMeta = 6;            // plane index of (k, z, wide, 0)
 constexpr uint32_t kXdLo = 7;              // first level-2 plane
 constexpr float kLoInv = 1.1920928955078125e-07f;  // 2^-23, the weight of level 2
 
-// The wide test on c1 = sum_e min(|A_e|, amax >> 4) and c2 = sum_e
-// min(|A_e|, amax >> 6): both bounds of the remainder below 3 (amax >> 6).
+// The wide test, in two stages.  maybe_wide: the bound from the magnitude
+// sum asum = sum_e |A_e| falls below 3 (amax >> 6); block_wide: so do the
+// bounds from c1 = sum_e min(|A_e|, amax >> 4) and c2 = sum_e min(|A_e|,
+// amax >> 6) (needed only when maybe_wide holds).
+__device__ __forceinline__ bool maybe_wide(int amax, int asum) { return asum - 6 * amax < 3 * (amax >> 6); }
 __device__ __forceinline__ bool block_wide(int amax, int c1, int c2) {
     const int t1 = amax >> 4, t2 = amax >> 6;
     return c1 - 6 * t1 < 3 * t2 && c2 - 6 * t2 < 3 * t2;
@@ -112,9 +117,13 @@ __device__ inline void prep_lane(float v, uint32_t c, bool store, uint32_t pad, 
     const int xi = (int)ar;
     const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
     const int ax = xi < 0 ? -xi : xi;
-    const int c1 = half_sum_i(min(ax, amax >> 4));
-    const int c2 = half_sum_i(min(ax, amax >> 6));
-    const bool wide = !bad && block_wide(amax, c1, c2);
+    const bool maybe = !bad && maybe_wide(amax, half_sum_i(ax));
+    bool wide = false;
+    if (__ballot(maybe) != 0ull) {  // wave-uniform: every lane takes part in the sums
+        const int c1 = half_sum_i(min(ax, amax >> 4));
+        const int c2 = half_sum_i(min(ax, amax >> 6));
+        wide = maybe && block_wide(amax, c1, c2);
+    }
     const int sh = 4 * (e & 7);
     const int q = e & 7, i = e >> 3;
     // Packs one 6-digit value per lane into plane dwords (8-lane OR) and
@@ -205,25 +214,34 @@ __device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[13
     float m;
     const int k = block_k(mb, bad, m);
     const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
-    const int t1 = amax >> 4, t2 = amax >> 6;
     uint32_t pl[6][4];
-    int c1 = 0, c2 = 0;
+    int asum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint32_t u[8], p8[6];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int a = bad ? 0 : (int)rintf(ldexpf(v[8 * i + e], k));
-            const int ax = a < 0 ? -a : a;
-            c1 += min(ax, t1);
-            c2 += min(ax, t2);
+            asum += a < 0 ? -a : a;
             u[e] = (uint32_t)(a + (int)kDigitBias);
         }
         planes8(u, p8);
 #pragma unroll
         for (int p = 0; p < 6; ++p) pl[p][i] = p8[p];
     }
-    const bool wide = !bad && block_wide(amax, c1, c2);
+    bool wide = false;
+    if (!bad && maybe_wide(amax, asum)) {
+        const int t1 = amax >> 4, t2 = amax >> 6;
+        int c1 = 0, c2 = 0;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const int a = (int)rintf(ldexpf(v[e], k));
+            const int ax = a < 0 ? -a : a;
+            c1 += min(ax, t1);
+            c2 += min(ax, t2);
+        }
+        wide = block_wide(amax, c1, c2);
+    }
 #pragma unroll
     for (int p = 0; p < 6; ++p) out[p] = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
     out[kXdMeta] = make_uint4((uint32_t)k, __float_as_uint(bad ? __builtin_nanf("") : 0.0f), (uint32_t)wide, 0u);
@@ -253,13 +271,17 @@ __device__ __forceinline__ void prep_block(const float (&v)[32], uint4 (&out)[13
 
 // prep_block split over the 4 lanes of an aligned lane quad: lane i of the
 // quad holds elements 8i..8i+7 of the block in v and gets dword i of every
-// level-1 plane (pl, already XORed with 0x88888888) and the block's meta
-// words (k, z, wide).  The block maximum and clamped magnitude sums are combined
+// level-1 plane (pl, already XORed with 0x88888888), the block's k and z
+// words, its level-1 maximum amax and maybe = maybe_wide (the cheap first
+// stage of the wide test).  The block maximum and magnitude sum are combined
 // across the quad, so all 4 lanes must call it together; the digits are
-// those of prep_block bit for bit.  prep_quarter_lo gives the same lane's
-// dwords of the level-2 planes of a wide block.
+// those of prep_block bit for bit.  quarter_wide completes the wide test
+// (the flag of prep_block), and prep_quarter_lo gives the same lane's dwords
+// of the level-2 planes of a wide block.  The second stage is kept apart so
+// a caller converting several blocks per lane runs it once, after all of
+// them, and only when some lane of the wave needs it.
 __device__ __forceinline__ void prep_quarter(const float (&v)[8], uint32_t (&pl)[6], uint32_t& k_out,
-                                             uint32_t& z_out, uint32_t& wide_out) {
+                                             uint32_t& z_out, int& amax_out, bool& maybe_out) {
     uint32_t mb = 0u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) mb = __builtin_elementwise_max(mb, __float_as_uint(v[e]) << 1);
@@ -268,23 +290,37 @@ __device__ __forceinline__ void prep_quarter(const float (&v)[8], uint32_t (&pl)
     float m;
     const int k = block_k(mb, bad, m);
     const int amax = bad ? 0 : (int)rintf(ldexpf(m, k));
-    const int t1 = amax >> 4, t2 = amax >> 6;
     uint32_t u[8];
-    int c1 = 0, c2 = 0;
+    int asum = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int a = bad ? 0 : (int)rintf(ldexpf(v[e], k));
-        const int ax = a < 0 ? -a : a;
-        c1 += min(ax, t1);
-        c2 += min(ax, t2);
+        asum += a < 0 ? -a : a;
         u[e] = (uint32_t)(a + (int)kDigitBias);
     }
     planes8(u, pl);
-    c1 = quad_sum_i(c1);
-    c2 = quad_sum_i(c2);
+    asum = quad_sum_i(asum);
     k_out = (uint32_t)k;
     z_out = __float_as_uint(bad ? __builtin_nanf("") : 0.0f);
-    wide_out = (uint32_t)(!bad && block_wide(amax, c1, c2));
+    amax_out = amax;
+    maybe_out = !bad && maybe_wide(amax, asum);
+}
+
+// Second stage of the wide test for a block prep_quarter converted (k,
+// amax, maybe from it); all 4 lanes of the quad call it together.
+__device__ __forceinline__ bool quarter_wide(const float (&v)[8], int k, int amax, bool maybe) {
+    const int t1 = amax >> 4, t2 = amax >> 6;
+    int c1 = 0, c2 = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int a = maybe ? (int)rintf(ldexpf(v[e], k)) : 0;
+        const int ax = a < 0 ? -a : a;
+        c1 += min(ax, t1);
+        c2 += min(ax, t2);
+    }
+    c1 = quad_sum_i(c1);
+    c2 = quad_sum_i(c2);
+    return maybe && block_wide(amax, c1, c2);
 }
 
 __device__ __forceinline__ void prep_quarter_lo(const float (&v)[8], int k, uint32_t (&pl2)[6]) {

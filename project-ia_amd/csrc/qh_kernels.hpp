@@ -142,6 +142,12 @@ hipError_t launch_causal_mask(float* m, uint32_t n, uint32_t ld, float mask_valu
 // y = silu(x) (u == nullptr) or silu(x) * u.
 hipError_t launch_silu(const float* x, const float* u, float* y, uint32_t N, hipStream_t s);
 hipError_t launch_softmax(const float* x, float* y, uint32_t N, hipStream_t s);
+// Softmax in the reference's exact summation order (k_sample.hip): bit-exact
+// with q_softmax_f32_avx2 except where the N % 8 tail's libm expf differs
+// from the device's.  ws holds softmax_exact_ws_bytes(N) bytes (less, down
+// to its dense minimum, makes the sum dense); x may alias y.
+size_t softmax_exact_ws_bytes(uint32_t N);
+hipError_t launch_softmax_exact(const float* x, float* y, uint32_t N, void* ws, size_t ws_bytes, hipStream_t s);
 // op 0: o = a + b; op 1: o = a * b.
 hipError_t launch_binary(const float* a, const float* b, float* o, uint32_t N, int op, hipStream_t s);
 hipError_t launch_argmax(const float* x, uint32_t N, uint32_t* out, hipStream_t s);

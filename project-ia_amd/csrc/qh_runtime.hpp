@@ -47,9 +47,17 @@ struct Device {
     // Partials of the multi-workgroup softmax/argmax used by the entry points
     // that take no workspace (allocated once at initialization).
     float* reduce_ws = nullptr;
+    // Digit workspace of the GEMV entry points called without one (inputs
+    // up to kLibGemvMaxN wide; allocated once at initialization).
+    void* gemv_ws = nullptr;
 };
 
-constexpr size_t kReduceWsBytes = 32768;
+constexpr size_t kReduceWsBytes = 65536;
+constexpr uint32_t kLibGemvMaxN = 1u << 20;
+
+// The no-allocation LM-head entry point's scratch address on device `dev`
+// (taken once, with that device current; api_noalloc.hip).
+q_error_code noalloc_scratch_init(int dev);
 
 // Returns Q_OK and the initialized device, or an error if no GPU is usable.
 q_error_code device(Device** out);
@@ -90,8 +98,13 @@ q_error_code validate_gemv(const q_tensor* W, const float* x, const float* y);
 // need a digit workspace, taken from the library's own allocation only when
 // may_allocate (else the call fails).
 size_t gemv_softmax_ws_bytes(uint32_t M);
+// need_ws: a NULL workspace is refused with the other NULL arguments.
 q_error_code validate_gemv_softmax(const q_tensor* W, const float* x, const float* logits, const float* probs,
-                                   const uint32_t* index_out);
+                                   const uint32_t* index_out, bool need_ws, const void* workspace);
+// After validation: every operand (and a non-NULL workspace) is device
+// memory of the extent the launches touch, else Q_ERR_INVALID_ARG.
+q_error_code check_gemv_softmax_memory(const q_tensor* W, const float* x, const float* logits, const float* probs,
+                                       const uint32_t* index_out, const void* workspace);
 q_error_code gemv_softmax_argmax_run(const q_tensor* W, const float* x, float* logits, float* probs,
                                      uint32_t* index_out, void* workspace, bool may_allocate, hipStream_t st);
 

@@ -187,10 +187,13 @@ def test_decode_unfused_wide_dim(qa, tmp_path):
 
 
 def test_build_graph_rejects_unbuilt_configs(qa, tmp_path):
-    """GQA groups other than 1/2/4/8 are refused at llama_build_graph with
-    Q_ERR_INVALID_CONFIG (not at the first step)."""
+    """GQA groups other than 1/2/4/8, and FFN widths above 32768 (the prefill
+    GEMM's row limit), are refused at llama_build_graph with
+    Q_ERR_INVALID_CONFIG (not at the first step or prompt)."""
     for i, h in enumerate([qa.QorusHeader(vocab=50, dim=384, hidden=256, n_layers=1, n_heads=3, n_kv=1, max_seq=16),
                            qa.QorusHeader(vocab=50, dim=1536, hidden=256, n_layers=1, n_heads=12, n_kv=2,
+                                          max_seq=16),
+                           qa.QorusHeader(vocab=50, dim=128, hidden=32800, n_layers=1, n_heads=1, n_kv=1,
                                           max_seq=16)]):
         path = tmp_path / f"bad{i}.qorus"
         qa.synthetic.write_synthetic_model(path, h, 16)
@@ -396,3 +399,47 @@ def test_decode_config4_full_depth(qa, tmp_path):
             m.close()
         if d != str(tmp_path):
             shutil.rmtree(d, ignore_errors=True)
+
+
+def _hip_free_bytes():
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_no_device_allocation_after_build_graph(qa, tmp_path):
+    """After llama_build_graph (and the first decode step, which captures the
+    step's graph), the first prompt through llama_forward, the first device
+    sampled generation and a GEMV wider than the in-kernel conversion with a
+    NULL workspace allocate no device memory: hipMemGetInfo's free bytes do
+    not change across them."""
+    import ctypes as C
+    h = qa.QorusHeader(vocab=1000, dim=512, hidden=1024, n_layers=2, n_heads=4, n_kv=1, max_seq=256)
+    m, blob, kv = build(qa, tmp_path, h, 41, 20)
+    lib = qa.lib()
+    M, N = 64, 32768
+    rng = orc.rng_for(41, 5)
+    dW = qa.DeviceBuffer.from_numpy(orc.gen_q4(M, N, rng))
+    dx = qa.DeviceBuffer.from_numpy(orc.gen_f32(N, rng))
+    dy = qa.DeviceBuffer(M * 4)
+    t = qa.q4_tensor(dW.ptr, M, N)
+    try:
+        m.forward([3], 20)  # the decode step's graph is captured here
+        qa.check(lib.qh_device_synchronize())
+        f0 = _hip_free_bytes()
+        m.forward([int(v) for v in rng.integers(0, h.vocab, 40)], 21)      # first prompt
+        f1 = _hip_free_bytes()
+        m.generate_sampled(7, 61, 4, 0.8, 40, 0.95)                        # first sampled loop
+        f2 = _hip_free_bytes()
+        qa.check(lib.qh_gemv_q4_f32(t.addr, dx.ptr, dy.ptr, None, None), "gemv, NULL workspace")
+        qa.check(lib.qh_device_synchronize())
+        f3 = _hip_free_bytes()
+        print(f"free bytes: {f0} {f1} {f2} {f3}")
+        assert f0 == f1 == f2 == f3, (f0 - f1, f1 - f2, f2 - f3)
+        # the wide GEMV ran on the library's workspace: its result is right
+        y64, cond = orc.gemv_f64(orc.gen_q4(M, N, orc.rng_for(41, 5)), M, N, dx.download(np.float32, (N,)))
+        assert np.max(np.abs(dy.download(np.float32, (M,)) - y64) / cond) <= 1e-5
+    finally:
+        m.close()

@@ -63,6 +63,49 @@ def test_noalloc_equals_workspace_form(qa):
         assert ig == iw == int(np.argmax(lw)), (h.M, h.N, ig, iw)
 
 
+def test_noalloc_under_graph_capture(qa):
+    """The no-alloc calls captured into a HIP graph (thread-local capture
+    mode, which refuses device allocations), then the graph replayed three
+    times with eager clears of the outputs in between: every replay gives
+    the workspace form's bits."""
+    lib = qa.lib()
+    heads = [LmHead(qa, M, N, 950 + i) for i, (M, N) in enumerate(CASES)]
+    want = []
+    for h in heads:
+        ws = qa.DeviceBuffer(lib.qh_gemv_softmax_workspace_bytes(h.M))
+        qa.check(lib.qh_gemv_q4_f32_softmax_argmax(h.t.addr, h.dx.ptr, h.logits.ptr, h.probs.ptr, h.idx.ptr,
+                                                   ws.ptr, None), "workspace form")
+        qa.check(lib.qh_device_synchronize())
+        want.append(h.outputs())
+    st = qa.Stream()
+    qa.check(lib.qh_stream_begin_capture(st.handle), "begin capture")
+    for h in heads:
+        rc = lib.qh_gemv_q4_f32_softmax_argmax_noalloc(h.t.addr, h.dx.ptr, h.logits.ptr, h.probs.ptr,
+                                                       h.idx.ptr, st.handle)
+        if rc != 0:
+            import ctypes as C
+            g = C.c_void_p()
+            lib.qh_stream_end_capture(st.handle, C.byref(g))
+            qa.check(rc, "noalloc under capture")
+    import ctypes as C
+    graph = C.c_void_p()
+    qa.check(lib.qh_stream_end_capture(st.handle, C.byref(graph)), "end capture")
+    try:
+        for rep in range(3):
+            for h in heads:
+                h.logits.zero(); h.probs.zero(); h.idx.zero()
+            qa.check(lib.qh_device_synchronize())
+            qa.check(lib.qh_graph_launch(graph.value, st.handle), "replay")
+            st.sync()
+            for h, (lw, pw, iw) in zip(heads, want):
+                lg, pg, ig = h.outputs()
+                assert np.array_equal(_bits(lg), _bits(lw)), (rep, h.M, h.N)
+                assert np.array_equal(_bits(pg), _bits(pw)), (rep, h.M, h.N)
+                assert ig == iw, (rep, h.M, h.N)
+    finally:
+        lib.qh_graph_destroy(graph.value)
+
+
 def test_noalloc_errors(qa):
     lib = qa.lib()
     f = lib.qh_gemv_q4_f32_softmax_argmax_noalloc
@@ -72,5 +115,13 @@ def test_noalloc_errors(qa):
     assert f(g.t.addr, g.dx.ptr, g.logits.ptr, None, g.idx.ptr, None) == -10
     assert f(g.t.addr, g.dx.ptr, g.logits.ptr, g.probs.ptr, None, None) == -10
     assert f(g.t.addr, g.dx.ptr, g.logits.ptr, g.logits.ptr, g.idx.ptr, None) == -11
+    # operands that are not device memory of the required extent: refused
+    hx = orc.aligned_copy(orc.gen_f32(256, orc.rng_for(9)))
+    assert f(g.t.addr, hx.ctypes.data, g.logits.ptr, g.probs.ptr, g.idx.ptr, None) == -10
+    short = qa.DeviceBuffer(32 * 4)
+    assert f(g.t.addr, g.dx.ptr, g.logits.ptr, short.ptr, g.idx.ptr, None) == -10
+    hw = orc.aligned_copy(orc.gen_q4(64, 256, orc.rng_for(10)).reshape(-1))
+    th = qa.q4_tensor(hw.ctypes.data, 64, 256)
+    assert f(th.addr, g.dx.ptr, g.logits.ptr, g.probs.ptr, g.idx.ptr, None) == -10
     assert f(g.t.addr, g.dx.ptr, g.logits.ptr, g.probs.ptr, g.idx.ptr, None) == 0
     assert lib.qh_device_synchronize() == 0
