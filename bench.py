@@ -17,9 +17,14 @@ value  = algorithmic bytes of the K timed steps / wall time of those steps,
          (weights + 4*N + 4*M) = 136,642,560 B.
 roofline = the dominant kernel (the fused W_gate|W_up GEMV launch), timed
          with HIP events on its stream around a graph of K back-to-back
-         launches (rotating the weight sets): achieved = its algorithmic
-         bytes / (elapsed / K), vs 8 TB/s.  The same K-launch graph times
-         each of the four launches for the "kernels" breakdown.
+         launches: achieved = its algorithmic bytes / (elapsed / K), vs
+         8 TB/s.  The same K-launch graph times each of the four launches
+         for the "kernels" breakdown; each launch shape rotates >= 300 MB of
+         distinct weight copies (so the 256 MB MALL serves no repeat), and
+         each line carries the time of a device-to-device copy of the same
+         bytes (its "copy floor", which moves twice the bytes: read + write).
+config1 = BASELINE config 1, one 4096x4096 GEMV from fp32 x, timed the same
+         way over 32 rotated copies.
 cpu_baseline = the reference's own q_gemv_q4_f32_avx2 (compiled from its
          sources into oracle/_ref) running the same 7-matrix set on one
          pinned host core of this machine, for a bounded sample.
@@ -48,6 +53,7 @@ DIM, KV, HID = 4096, 1024, 14336
 SHAPES = [("wq", DIM, DIM), ("wk", KV, DIM), ("wv", KV, DIM), ("wo", DIM, DIM),
           ("w_gate", HID, DIM), ("w_up", HID, DIM), ("w_down", DIM, HID)]
 LAYERS = 4
+ROT_BYTES = 300 << 20  # distinct weight bytes each timed launch shape rotates over
 
 
 def alg_bytes(M, N):
@@ -138,15 +144,41 @@ def run_gpu(args):
     wall = t1 - t0
     graphs = [warm, timed]
 
-    # ---- per-launch kernel time: K launches of one GEMV group (rotating the
-    # weight sets) captured back to back in one graph, HIP events on the
-    # stream around its replay; mean = elapsed / K.  Inside a graph the
-    # launches follow each other with no dispatch gap, so this is the
-    # kernel's own duration (what rocprofv3 --kernel-trace reports).
-    def time_group(xk, mats):
+    # ---- per-launch kernel time: K launches of one GEMV group captured back
+    # to back in one graph, HIP events on the stream around its replay;
+    # mean = elapsed / K.  Inside a graph the launches follow each other with
+    # no dispatch gap, so this is the kernel's own duration (what rocprofv3
+    # --kernel-trace reports).  Each launch shape rotates at least ROT_BYTES
+    # of distinct weight copies (device copies of the layer sets), so the
+    # 256 MB MALL cannot serve a repeat.
+    kbytes = {"qkv": sum(alg_bytes(M, N) for k, M, N in SHAPES if k in ("wq", "wk", "wv")),
+              "wo": alg_bytes(DIM, DIM), "gate_up": GATE_UP_BYTES, "down": alg_bytes(DIM, HID)}
+    extra = []  # keeps the copies alive
+
+    def rotated(mats, min_sets=0):
+        """Tensor sets of `mats` totalling >= ROT_BYTES (and at least
+        min_sets of them): the LAYERS generated sets, then device copies."""
+        sets = [{m: L.t[m] for m in mats} for L in layers]
+        wbytes = sum(M * (N // 32) * 20 for k, M, N in SHAPES if k in mats)
+        i = 0
+        while len(sets) * wbytes < ROT_BYTES or len(sets) < min_sets:
+            src = layers[i % LAYERS]
+            cp = {}
+            for m in mats:
+                M, N = next((M, N) for k, M, N in SHAPES if k == m)
+                b = qa.DeviceBuffer(M * (N // 32) * 20)
+                qa.check(lib.qh_memcpy_dtod(b.ptr, src.bufs[m].ptr, b.nbytes, s), "copy")
+                extra.append(b)
+                cp[m] = qa.q4_tensor(b.ptr, M, N)
+            sets.append(cp)
+            i += 1
+        stream.sync()
+        return sets
+
+    def time_graph(enqueue, n):
         qa.check(lib.qh_stream_begin_capture(s), "begin_capture")
-        for i in range(args.steps):
-            gemv_group(layers[i % LAYERS], xk, mats)
+        for i in range(n):
+            enqueue(i)
         g = C.c_void_p()
         qa.check(lib.qh_stream_end_capture(s, C.byref(g)), "end_capture")
         qa.check(lib.qh_graph_launch(g.value, s))  # warm
@@ -156,20 +188,64 @@ def run_gpu(args):
         e1.record(stream)
         stream.sync()
         lib.qh_graph_destroy(g.value)
-        return e0.elapsed_ms(e1) / args.steps
+        return e0.elapsed_ms(e1) / n
 
-    per_kernel = {name: time_group(xk, mats) for name, xk, mats in groups}
-    mean_ms = per_kernel["gate_up"]
-    kbytes = {"qkv": sum(alg_bytes(M, N) for k, M, N in SHAPES if k in ("wq", "wk", "wv")),
-              "wo": alg_bytes(DIM, DIM), "gate_up": GATE_UP_BYTES, "down": alg_bytes(DIM, HID)}
+    def time_group(xk, mats, sets):
+        def enq(i):
+            st = sets[i % len(sets)]
+            Ws = ptr_array([st[m].addr for m in mats])
+            ys = ptr_array([outs[m].ptr for m in mats])
+            qa.check(lib.qh_gemv_q4_f32_multi(Ws, None, ys, len(mats), xin[xk].ptr, ws[xk].ptr, s), "gemv")
+        return time_graph(enq, max(args.steps, 2 * len(sets)))
+
+    # The copy floor of a launch: a device-to-device copy of the launch's
+    # algorithmic bytes, from a rotated source region into a rotated
+    # destination region (each >= ROT_BYTES of distinct addresses), timed
+    # the same way.  It moves twice the bytes the GEMV reads (read + write),
+    # so copy_us / us > 1 means the GEMV streams its bytes faster than a
+    # copy of them completes.
+    pool_bytes = ROT_BYTES + (80 << 20)
+    src_pool, dst_pool = qa.DeviceBuffer(pool_bytes), qa.DeviceBuffer(pool_bytes)
+
+    def time_copy(nbytes):
+        nbytes = (nbytes + 255) & ~255
+        slots = max(2, pool_bytes // nbytes)
+
+        def enq(i):
+            off = (i % slots) * nbytes
+            qa.check(lib.qh_memcpy_dtod(dst_pool.ptr + off, src_pool.ptr + off, nbytes, s), "copy")
+        return time_graph(enq, max(args.steps, 2 * slots))
+
     breakdown = {}
-    for name, ms in per_kernel.items():
+    per_kernel = {}
+    for name, xk, mats in groups:
+        sets = rotated(mats)
+        ms = time_group(xk, mats, sets)
+        per_kernel[name] = ms
         us = ms * 1e3
-        breakdown[name] = {"us": round(us, 2), "GB_s": round(kbytes[name] / (us * 1e-6) / 1e9, 1)}
+        cus = time_copy(kbytes[name]) * 1e3
+        gbs = kbytes[name] / (us * 1e-6) / 1e9
+        breakdown[name] = {"us": round(us, 2), "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                           "copies_rotated": len(sets), "rotated_MB": round(len(sets) * kbytes[name] / 1e6),
+                           "copy_floor_us": round(cus, 2), "frac_of_copy_floor": round(cus / us, 3)}
+        log(f"[bench] {name}: {us:.2f} us ({gbs:.0f} GB/s, {len(sets)} copies); copy of the same bytes {cus:.2f} us")
+    mean_ms = per_kernel["gate_up"]
     for g in graphs:
         lib.qh_graph_destroy(g)
     achieved = GATE_UP_BYTES / (mean_ms * 1e-3) / 1e9
-    return wall, achieved, mean_ms, breakdown
+    # one 4096 x 4096 GEMV from fp32 x (the Wo shape as a
+    # standalone launch), >= 32 rotated copies.
+    c1_sets = rotated(["wo"], min_sets=32)
+    c1_ms = time_group("o", ["wo"], c1_sets)
+    c1_bytes = alg_bytes(DIM, DIM)
+    c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
+    config1 = {"workload": "config1: one Q4_0 GEMV 4096x4096 from fp32 x ~ N(0,1) (digit planes made in the launch)",
+               "us": round(c1_ms * 1e3, 2), "alg_bytes": c1_bytes, "GB_s": round(c1_gbs, 1),
+               "frac_hbm_peak": round(c1_gbs / HBM_PEAK_GBS, 4), "copies_rotated": len(c1_sets),
+               "copy_floor_us": breakdown["wo"]["copy_floor_us"],
+               "frac_of_copy_floor": round(breakdown["wo"]["copy_floor_us"] / (c1_ms * 1e3), 3)}
+    log(f"[bench] config1: {c1_ms * 1e3:.2f} us ({c1_gbs:.0f} GB/s, {len(c1_sets)} copies)")
+    return wall, achieved, mean_ms, breakdown, config1
 
 
 def run_cpu_baseline(seconds):
@@ -879,7 +955,7 @@ def main():
         run_traffic()
         return
 
-    wall, achieved, kern_ms, breakdown = run_gpu(args)
+    wall, achieved, kern_ms, breakdown, config1 = run_gpu(args)
     ms_per_step = wall / args.steps * 1e3
     value = STEP_BYTES * args.steps / wall / 1e9
     cpu = None if args.no_cpu else run_cpu_baseline(args.cpu_seconds)
@@ -910,6 +986,7 @@ def main():
                      "kernel": "k_gemv (fused W_gate|W_up, 28672x4096)",
                      "alg_bytes_per_launch": GATE_UP_BYTES, "mean_launch_us": round(kern_ms * 1e3, 2)},
         "kernels": breakdown,
+        "config1": config1,
         "cpu_baseline": cpu,
         "lmhead": lmhead,
         "decode": decode,
