@@ -940,6 +940,8 @@ def main():
     ap.add_argument("--summarize-attn-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/attention_traffic.json from two --pmc passes over the decode leg")
     ap.add_argument("--traffic-cmd", default="", help="command line recorded with the summary")
+    ap.add_argument("--only", choices=("prefill", "decode", "lmhead"),
+                    help="run one leg alone and print its JSON (for profiler runs; not the bench line)")
     args = ap.parse_args()
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic, args.traffic_cmd)
@@ -953,6 +955,10 @@ def main():
         sys.exit(2)
     if args.traffic:
         run_traffic()
+        return
+    if args.only:
+        leg = {"prefill": run_prefill, "decode": run_decode, "lmhead": run_lmhead}[args.only]
+        print(json.dumps({"leg": args.only, "result": leg(args)}), flush=True)
         return
 
     wall, achieved, kern_ms, breakdown, config1 = run_gpu(args)
