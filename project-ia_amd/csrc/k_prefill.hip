@@ -13,6 +13,7 @@
 
 #include <algorithm>
 
+#include <cfloat>
 #include <cstdint>
 #include <type_traits>
 
@@ -22,6 +23,7 @@
 namespace qh {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kPHd = 128;  // head_dim the prefill kernels are written for
 
@@ -128,7 +130,66 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 }
 
 // ---------------------------------------------------------------------------
-// Causal prefill attention on v_mfma_f32_16x16x4_f32.
+// Keys as fp16 hi/lo rows for the attention's q.k on fp16 matrix cores.
+// Row j of KV head h (keys 0 .. n_keys-1) is scaled by 2^e, e chosen per
+// row so that max|k'| lies in [2^14, 2^15) (e = 0 for an all-zero or
+// non-finite row), and split as hi = rn(k'), lo = rn(k' - hi) (the
+// subtraction is exact in fp32): 22 significant bits of every element within
+// 2^17 of the row maximum, steps of 2^-24 (of k') below that.  With each
+// row goes a flag: the key's V row holds a NaN or an infinity (its P.V terms
+// must then be formed even where e_j = 0, as 0 * v_j is NaN).  Layout: halfs
+// [n_kv][max_seq][hi 0..127 | lo 0..127], then int32 2e + flag [n_kv][max_seq].
+// One 32-lane half of a wave per row, one float4 of K and of V per lane.
+// ---------------------------------------------------------------------------
+size_t prefill_khl_bytes(uint32_t n_kv, uint32_t max_seq) {
+    const size_t rows = (size_t)n_kv * max_seq;
+    return ((rows * 2 * kPHd * 2 + 255) & ~(size_t)255) + rows * 4;
+}
+
+__host__ __device__ inline int* khl_meta(void* khl, uint32_t n_kv, uint32_t max_seq) {
+    const size_t rows = (size_t)n_kv * max_seq;
+    return reinterpret_cast<int*>(static_cast<uint8_t*>(khl) + ((rows * 2 * kPHd * 2 + 255) & ~(size_t)255));
+}
+
+// Exponent e with max|x * 2^e| in [2^14, 2^15) for a finite m = max|x| > 0,
+// else 0.
+__device__ __forceinline__ int split_exp(float m) {
+    return (m > 0.0f && m <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+}
+
+__global__ __launch_bounds__(256) void k_prefill_khl(const float* __restrict__ kv, uint32_t n_keys, uint32_t max_seq,
+                                                     _Float16* __restrict__ khl, int* __restrict__ meta) {
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t j = blockIdx.x * 8u + (threadIdx.x >> 5), c = threadIdx.x & 31u;
+    if (j >= n_keys) return;  // uniform over the row's 32 lanes
+    const size_t row = (size_t)kvh * max_seq + j;
+    const float4 x = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + 4 * c);
+    const float4 vx = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + kPHd + 4 * c);
+    const bool vbad = !(fabsf(vx.x) <= FLT_MAX && fabsf(vx.y) <= FLT_MAX && fabsf(vx.z) <= FLT_MAX &&
+                        fabsf(vx.w) <= FLT_MAX);
+    const uint64_t vb = __ballot(vbad);
+    const bool row_vbad = ((threadIdx.x & 32) ? (uint32_t)(vb >> 32) : (uint32_t)vb) != 0u;
+    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    if (!(x.x == x.x && x.y == x.y && x.z == x.z && x.w == x.w)) m = INFINITY;  // NaN: no scaling
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    const int e = split_exp(m);
+    const float v[4] = {ldexpf(x.x, e), ldexpf(x.y, e), ldexpf(x.z, e), ldexpf(x.w, e)};
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hi[i] = (_Float16)v[i];
+        lo[i] = (_Float16)(v[i] - (float)hi[i]);
+    }
+    _Float16* dst = khl + row * (2 * kPHd) + 4 * c;
+    *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(hi);
+    *reinterpret_cast<uint2*>(dst + kPHd) = *reinterpret_cast<const uint2*>(lo);
+    if (c == 0) meta[row] = 2 * e + (row_vbad ? 1 : 0);
+}
+
+// ---------------------------------------------------------------------------
+// Causal prefill attention: q.k on fp16 matrix cores (v_mfma_f32_16x16x32_f16
+// on hi/lo parts), P.V on v_mfma_f32_16x16x4_f32.
 //
 // Workgroup: 16 queries (a query tile) x HG of the G query heads of one KV
 // head, two waves per head, each taking half of every staged 64-key block (so
@@ -144,14 +205,20 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 // a first pass over the keys and the scores are recomputed (bit-identically)
 // in the second; the two halves' maxima, sums and P.V partials meet in LDS.
 //
-// Fragment layouts (16x16x4: lane l feeds A[l%16][l/16] and B[l/16][l%16];
-// D[4*(l/16)+r][l%16] lands in register r of lane l):
-//  * scores S^T[key][query] = K . Q^T: the contraction index of MFMA step kk
-//    in lane group g = l/16 is element 32g + kk of the head (any pairing of
-//    the 128 elements to the 32 steps x 4 groups works when A and B agree),
-//    so each lane reads 32 consecutive floats of one K row and keeps 32
-//    consecutive floats of its query;
-//  * the result gives lane l query l%16 and keys 4g + r of the 16-key
+// q.k: q rows are scaled and split like the keys (k_prefill_khl; the query's
+// exponent from its own 128 elements), and each dot is
+// (hi.hi) + (hi.lo + lo.hi) over the scaled parts (the lo.lo term, at most
+// 2^-22 of |q||k| per element, is left out), times 2^-(e_q + e_k), exact.
+//
+// Fragment layouts (D[4*(l/16)+r][l%16] lands in register r of lane l):
+//  * scores S^T[key][query] = K . Q^T on 16x16x32 f16 (lane l feeds 8
+//    consecutive contraction slots 8*(l/16) .. +7 of A row l%16 and of B
+//    column l%16): slot i of step c in lane group g = l/16 is element
+//    32g + 8c + i of the head (any pairing of the 128 elements works when A
+//    and B agree), so each lane reads 32 consecutive halfs of one key row's
+//    hi and lo parts and keeps 32 consecutive elements of its query;
+//  * P.V on 16x16x4 f32 (lane l feeds A[l%16][l/16] and B[l/16][l%16]):
+//    the scores give lane l query l%16 and keys 4g + r of the 16-key
 //    block, which is exactly lane l's A fragment of O = P . V for step kk = r
 //    if step kk pairs lane group g with key 4g + kk; V is read in that key
 //    order, and output column d of tile t in lane l%16 is 4*(l%16) + t
@@ -162,13 +229,16 @@ constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
 
 template <uint32_t G, uint32_t HG>
-__global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs a) {
+__global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) void k_prefill_attn(const PrefillAttnArgs a) {
     static_assert(G % HG == 0, "head split");
     constexpr uint32_t NT = 128 * HG;
     constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
     static_assert(kLoads * NT == kAttnKS * (kPHd / 4), "stage/thread mismatch");
     static_assert(HG * 64 * 32 <= 2 * kAttnKS * kAttnRS, "the P.V exchange reuses the staging space");
-    __shared__ __attribute__((aligned(16))) float lkv[2][kAttnKS][kAttnRS];  // [0] K rows, [1] V rows
+    // [0]: key rows as fp16 hi (bytes 0..255) and lo (256..511); [1]: V rows
+    __shared__ __attribute__((aligned(16))) float lkv[2][kAttnKS][kAttnRS];
+    __shared__ __attribute__((aligned(16))) int lke[kAttnKS];  // the staged keys' exponents
+    __shared__ int lvb[kAttnKS];                              // and their V rows' non-finite flags
     __shared__ float xmax[2][HG][16], xsum[HG][16];
 
     const uint32_t n_qt = (a.T + 15) / 16;
@@ -187,6 +257,9 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
     const uint32_t n_stages = (n_keys + kAttnKS - 1) / kAttnKS;
     const size_t q_ld = (size_t)a.n_heads * kPHd;
     const float* kbase = a.kv + (size_t)kvh * a.max_seq * 2 * kPHd;
+    // key rows (hi|lo halfs, 128 floats' worth each) and exponents
+    const float* khbase = reinterpret_cast<const float*>(a.khl) + (size_t)kvh * a.max_seq * kPHd;
+    const int* kmbase = khl_meta(a.khl, a.n_kv, a.max_seq) + (size_t)kvh * a.max_seq;
 
     // This lane's query (B column li) and its 32 elements 32*lg .. 32*lg+31.
     const uint32_t my_t = t0 + li;
@@ -194,10 +267,16 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
     const uint32_t P = a.pos0 + my_t;  // attends keys 0..P
     const uint32_t S = P + 1u;
     const uint32_t Sv = S >= 8u ? (S & ~7u) : 0u;
-    float qv[32];
+    // Its scaled hi/lo parts, step c holding elements 32*lg + 8c .. +7, and
+    // its exponent (the max over the 4 lanes that hold the query).
+    h8v qh[4], ql[4];
+    int eq = 0;
     {
+        float qv[32];
         const float4* qr = reinterpret_cast<const float4*>(a.q + (size_t)(q_ok ? my_t : t_last) * q_ld +
                                                            (size_t)h * kPHd + 32 * lg);
+        float m = 0.0f;
+        bool nan = false;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const float4 v = qr[c];
@@ -206,6 +285,24 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
             qv[4 * c + 2] = q_ok ? v.z : 0.0f;
             qv[4 * c + 3] = q_ok ? v.w : 0.0f;
         }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            m = fmaxf(m, fabsf(qv[i]));
+            nan |= qv[i] != qv[i];
+        }
+        if (nan) m = INFINITY;  // no scaling
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        eq = split_exp(m);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = ldexpf(qv[8 * c + i], eq);
+                const _Float16 hv = (_Float16)v;
+                qh[c][i] = hv;
+                ql[c][i] = (_Float16)(v - (float)hv);
+            }
     }
 
     // Rows st*KS .. +KS-1 of K (and V): fetch into registers, then put into
@@ -214,7 +311,9 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
     // (vectors rather than arrays: arrays live across the loop stayed in
     // scratch memory)
     typedef float stage_v __attribute__((ext_vector_type(4 * kLoads)));
+    typedef int stage_e __attribute__((ext_vector_type(kLoads)));
     stage_v kr, vr;
+    stage_e km;  // 2e + V flag of the rows whose float4 0 this thread holds
     // mode: 0 = K rows, 1 = K and V rows, 2 = V rows
     using NoV = std::integral_constant<int, 0>;
     using WithV = std::integral_constant<int, 1>;
@@ -230,12 +329,14 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
             j = j < n_keys ? j : n_keys - 1u;
             const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)j * 2 * kPHd) + c;
             if constexpr (with_k) {
-                const float4 k4 = src[0];
+                // 16 bytes of the key's hi|lo row, moved as raw bits
+                const float4 k4 = reinterpret_cast<const float4*>(khbase + (size_t)j * kPHd)[c];
                 kr[4 * u] = k4.x;
                 kr[4 * u + 1] = k4.y;
                 kr[4 * u + 2] = k4.z;
                 kr[4 * u + 3] = k4.w;
             }
+            if (c == 0) km[u] = kmbase[j];
             if constexpr (with_v) {
                 const float4 v4 = src[kPHd / 4];
                 vr[4 * u] = v4.x;
@@ -252,9 +353,13 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
         for (uint32_t u = 0; u < kLoads; ++u) {
             const uint32_t i = threadIdx.x + u * NT;
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
-            if constexpr (with_k)
+            if constexpr (with_k) {
                 *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) =
                     make_float4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+                if (c == 0) lke[r] = km[u] >> 1;
+            }
+            if constexpr (with_v)
+                if (c == 0) lvb[r] = km[u] & 1;
             if constexpr (with_v)
                 *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) =
                     make_float4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
@@ -262,24 +367,26 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
     };
 
     // Scores of keys sub*16 .. sub*16+15 of the staged block (times scale
-    // applied by the caller): two accumulation chains, then their sum.
+    // applied by the caller): hi.hi and the two cross terms in two chains,
+    // their sum, then the exponents undone.
     auto scores = [&](uint32_t sub) -> f4v {
         f4v d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const float* kr = &lkv[0][sub * 16 + li][32 * lg];
+        const _Float16* kr = reinterpret_cast<const _Float16*>(&lkv[0][sub * 16 + li][0]) + 32 * lg;
 #pragma unroll
-        for (int c = 0; c < 8; c += 2) {
-            const float4 k0 = *reinterpret_cast<const float4*>(kr + 4 * c);
-            const float4 k1 = *reinterpret_cast<const float4*>(kr + 4 * c + 4);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.x, qv[4 * c + 0], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.x, qv[4 * c + 4], d1, 0, 0, 0);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.y, qv[4 * c + 1], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.y, qv[4 * c + 5], d1, 0, 0, 0);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.z, qv[4 * c + 2], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.z, qv[4 * c + 6], d1, 0, 0, 0);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0.w, qv[4 * c + 3], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1.w, qv[4 * c + 7], d1, 0, 0, 0);
+        for (int c = 0; c < 4; ++c) {
+            const h8v kh = *reinterpret_cast<const h8v*>(kr + 8 * c);
+            const h8v kl = *reinterpret_cast<const h8v*>(kr + kPHd + 8 * c);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], d1, 0, 0, 0);
         }
-        return d0 + d1;
+        f4v d = d0 + d1;
+        const int4 ek = *reinterpret_cast<const int4*>(&lke[sub * 16 + 4 * lg]);
+        d[0] = ldexpf(d[0], -(eq + ek.x));
+        d[1] = ldexpf(d[1], -(eq + ek.y));
+        d[2] = ldexpf(d[2], -(eq + ek.z));
+        d[3] = ldexpf(d[3], -(eq + ek.w));
+        return d;
     };
 
     // Row max over the 16 keys of d (scores of keys jb .. jb+15).
@@ -316,6 +423,12 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
             e[r] = ev;
             sum += ev;
         }
+        // A 16-key block whose e_j are 0 for every query of the tile adds
+        // exact zeros (0 * v_j for finite v_j): its P.V is skipped.  (The
+        // polynomial exp is 0 below about -2.18, so most keys of a peaked
+        // score row take no part.)
+        const bool nz = (e[0] != 0.0f) | (e[1] != 0.0f) | (e[2] != 0.0f) | (e[3] != 0.0f);
+        if (__ballot(nz || lvb[sub * 16 + li] != 0) == 0ull) return;  // wave-uniform
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const float* vr = &lkv[1][sub * 16 + 4 * lg + kk][0];
@@ -446,13 +559,18 @@ __global__ __launch_bounds__(128 * HG) void k_prefill_attn(const PrefillAttnArgs
 template <uint32_t G>
 static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
     constexpr uint32_t HG = G < 2 ? G : 2;  // heads per workgroup
+    const uint32_t n_keys = a.pos0 + a.T;
+    hipLaunchKernelGGL(k_prefill_khl, dim3((n_keys + 7) / 8, a.n_kv), dim3(256), 0, s, a.kv, n_keys, a.max_seq,
+                       static_cast<_Float16*>(a.khl), khl_meta(a.khl, a.n_kv, a.max_seq));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     const uint32_t n_qt = (a.T + 15) / 16;
     hipLaunchKernelGGL((k_prefill_attn<G, HG>), dim3(n_qt, a.n_kv * (G / HG)), dim3(128 * HG), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
-    if (a.T == 0 || a.n_kv == 0 || a.n_heads % a.n_kv != 0 || (uint64_t)a.pos0 + a.T > a.max_seq)
+    if (a.T == 0 || a.n_kv == 0 || a.n_heads % a.n_kv != 0 || (uint64_t)a.pos0 + a.T > a.max_seq || !a.khl)
         return hipErrorInvalidValue;
     switch (a.n_heads / a.n_kv) {
         case 1: return run_prefill_attention<1>(a, s);

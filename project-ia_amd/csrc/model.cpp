@@ -78,6 +78,7 @@ struct ModelPlan {
     float *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr;
     uint32_t* pf_tok = nullptr;
     void* pf_ws = nullptr;
+    void* pf_khl = nullptr;  // the prefill attention's fp16 hi/lo key rows (one layer)
     uint32_t* pinned_tok = nullptr;          // host staging for a chunk's tokens
 };
 
@@ -343,7 +344,7 @@ static q_error_code capture(ModelPlan* p, bool feedback, hipGraphExec_t* out) {
 // (silu(G) * U) (the SwiGLU product made where the GEMM converts its rows).
 // The last chunk ends with the LM head of its last row.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kPrefillRows = 512;  // tokens per prefill chunk
+constexpr uint32_t kPrefillRows = 2048;  // tokens per prefill chunk
 
 static size_t prefill_ws_bytes(const ModelPlan* p, uint32_t T) {
     const q_llama_config& c = p->cfg;
@@ -369,6 +370,7 @@ static q_error_code prefill_alloc(ModelPlan* p) {
     const size_t rd = (size_t)R * c.dim * 4, rk = (size_t)R * p->kvd * 4, rh = (size_t)R * c.hidden_dim * 4;
     const size_t o_x = carve(rd), o_x1 = carve(rd), o_q = carve(rd), o_k = carve(rk), o_v = carve(rk);
     const size_t o_o = carve(rd), o_g = carve(rh), o_u = carve(rh), o_t = carve((size_t)R * 4), o_ws = carve(ws);
+    const size_t o_kh = carve(prefill_khl_bytes(c.n_kv_heads, c.max_seq_len));
     if (!p->pinned_tok)
         QH_TRY(hipHostMalloc(reinterpret_cast<void**>(&p->pinned_tok), (size_t)R * 4, hipHostMallocDefault));
     QH_TRY(hipMalloc(&p->pf_arena, bytes));
@@ -383,6 +385,7 @@ static q_error_code prefill_alloc(ModelPlan* p) {
     p->pf_u = reinterpret_cast<float*>(A + o_u);
     p->pf_tok = reinterpret_cast<uint32_t*>(A + o_t);
     p->pf_ws = A + o_ws;
+    p->pf_khl = A + o_kh;
     p->pf_rows = R;
     return Q_OK;
 }
@@ -440,6 +443,7 @@ static hipError_t enqueue_prefill(ModelPlan* p, uint32_t T, uint32_t pos0, bool 
         aa.n_kv = c.n_kv_heads;
         aa.max_seq = c.max_seq_len;
         aa.scale = p->scale;
+        aa.khl = p->pf_khl;
         QH_E(launch_prefill_attention(aa, s));
         GemmSegs wo;
         wo.n = 1;

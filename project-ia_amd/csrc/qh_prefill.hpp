@@ -33,7 +33,11 @@ struct PrefillAttnArgs {
     float* o;               // [T][n_heads*128]
     uint32_t T, pos0, n_heads, n_kv, max_seq;
     float scale;            // 1/sqrtf(head_dim)
+    void* khl;              // scratch, prefill_khl_bytes(n_kv, max_seq): the keys as
+                            // scaled fp16 hi/lo rows and their exponents
 };
+// Bytes of PrefillAttnArgs::khl for a cache of n_kv heads x max_seq rows.
+size_t prefill_khl_bytes(uint32_t n_kv, uint32_t max_seq);
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s);
 
 }  // namespace qh

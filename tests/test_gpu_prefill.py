@@ -1,7 +1,7 @@
 """GPU parity of the batched prefill: llama_forward with seq_len > 1 (every
 projection on the MFMA GEMM with the RMSNorm / SwiGLU product made where it
 converts its rows, RoPE + KV-cache stores, causal attention of the prompt's
-queries over the cache on fp32 matrix cores, chunks of up to 512 tokens)
+queries over the cache on matrix cores, chunks of up to 2048 tokens)
 against the oracle's token-by-token decode steps (or_decode_step), which is
 what the prefill must equal: token t of the prompt attends the cached keys
 0 .. pos + t.
@@ -136,15 +136,17 @@ def test_prefill_small_tiles_with_k_splits(qa, tmp_path, T):
         m.close()
 
 
-def test_prefill_chunks_past_512_tokens(qa, tmp_path):
-    """A 600-token prompt at position 3: a 512-token chunk, then 88 tokens
-    whose queries attend the first chunk's keys from the cache."""
-    h = qa.QorusHeader(vocab=400, dim=256, hidden=512, n_layers=2, n_heads=2, n_kv=1, max_seq=640)
+@pytest.mark.parametrize("T", [600, 2100])
+def test_prefill_long_prompts_and_chunks(qa, tmp_path, T):
+    """A 600-token prompt at position 3 (one chunk), and a 2100-token one: a
+    2048-token chunk, then 52 tokens whose queries attend the first chunk's
+    keys from the cache."""
+    h = qa.QorusHeader(vocab=400, dim=256, hidden=512, n_layers=2, n_heads=2, n_kv=1, max_seq=T + 40)
     m, blob, kv = build(qa, tmp_path, h, 61, 3)
     try:
         ref = orc.DecodeOracle(blob, kv.copy())
-        toks = [int(t) for t in orc.rng_for(61, 2).integers(0, h.vocab, 600)]
-        check_prompt(qa, m, h, kv, ref, toks, 3, "600 tokens")
+        toks = [int(t) for t in orc.rng_for(61, 2).integers(0, h.vocab, T)]
+        check_prompt(qa, m, h, kv, ref, toks, 3, f"{T} tokens")
     finally:
         m.close()
 
@@ -218,13 +220,16 @@ def test_causal_mask_entry_points(qa):
     assert lib.qh_causal_mask_f32(d.ptr, 16, 16, -1.0, None) == -10  # 1 KB of rows, a 64-byte buffer
 
 
-def test_prefill_512_tokens_config4_widths(qa, tmp_path):
-    """The launch plan the bench's 512-token prompt times, checked: config-4
-    widths (d 4096, GQA 32/8 x 128, FFN 14336) with 2 layers and the
-    vocabulary cut to 1024, a 512-token prompt at position 0 (Q|K|V split-K
-    2, the 256/192-row cut of W_gate|W_up, W_down split 4, register-held
-    scores for 512 keys at GQA group 4), against the oracle's 511 cache
-    fills and last step (spread over host threads; the same bits as one).
+@pytest.mark.parametrize("T", [512, 2048])
+def test_prefill_config4_widths(qa, tmp_path, T):
+    """The launch plans the bench's 512- and 2048-token prompts time,
+    checked: config-4 widths (d 4096, GQA 32/8 x 128, FFN 14336) with 2
+    layers and the vocabulary cut to 1024, a T-token prompt at position 0
+    (for 512: Q|K|V split-K 2, the 256/192-row cut of W_gate|W_up, W_down
+    split 4, register-held scores for 512 keys at GQA group 4; for 2048 the
+    two-pass attention over up to 2048 keys), against the oracle's T - 1
+    cache fills and last step (spread over host threads; the same bits as
+    one).
     W_gate's block scales are divided by 4 (gates of std ~2 instead of ~8):
     the reference's SiLU jumps at g = -10 (its polynomial exp is 91.4 for
     5 < x <= 10 and 22026 above), so a gate within a few ulp of -10 takes
@@ -233,7 +238,7 @@ def test_prefill_512_tokens_config4_widths(qa, tmp_path):
     within 1e-4 of it, and the tokens holding them differed from the oracle
     by up to 1.3e-4 in the next layer's cache rows."""
     import os
-    h = qa.QorusHeader(vocab=1024, dim=4096, hidden=14336, n_layers=2, n_heads=32, n_kv=8, max_seq=520)
+    h = qa.QorusHeader(vocab=1024, dim=4096, hidden=14336, n_layers=2, n_heads=32, n_kv=8, max_seq=T + 8)
     path = tmp_path / "c4w.qorus"
     qa.synthetic.write_synthetic_model(path, h, 73)
     blob = np.fromfile(path, dtype=np.uint8)
@@ -249,11 +254,11 @@ def test_prefill_512_tokens_config4_widths(qa, tmp_path):
     orc.set_threads(min(16, os.cpu_count() or 1))
     try:
         ref = orc.DecodeOracle(blob, kv.copy())
-        toks = [int(t) for t in orc.rng_for(73, 3).integers(0, h.vocab, 512)]
-        tok = check_prompt(qa, m, h, kv, ref, toks, 0, "512 tokens, config-4 widths")
-        # a decode step after the prompt reads the 512 prefilled rows
-        lg = m.forward([tok], 512)
-        tok_ref, lg_ref = ref.step(tok, 512)
+        toks = [int(t) for t in orc.rng_for(73, 3).integers(0, h.vocab, T)]
+        tok = check_prompt(qa, m, h, kv, ref, toks, 0, f"{T} tokens, config-4 widths")
+        # a decode step after the prompt reads the T prefilled rows
+        lg = m.forward([tok], T)
+        tok_ref, lg_ref = ref.step(tok, T)
         assert rel_err(lg, lg_ref) <= 1e-4
         assert int(np.argmax(lg)) == tok_ref
     finally:
