@@ -361,7 +361,7 @@ def run_decode(args):
             m.generate_sampled(first_tok, DEC_POS, args.decode_warmup, 0.8, 40, 0.95)
             m.upload_kv(kv)
             _, ms_s = m.generate_sampled(first_tok, DEC_POS, steps, 0.8, 40, 0.95)
-        prefill = None if args.no_prompt else run_prompt(m, h, args.prompt_tokens)
+        prefills = [] if args.no_prompt else [run_prompt(m, h, T) for T in args.prompt_tokens]
         m.close()
         avg_ctx = DEC_POS + 1 + (steps - 1) / 2
         bpt = decode_bytes_per_token(ctx=int(round(avg_ctx)))
@@ -377,8 +377,8 @@ def run_decode(args):
                "sampled_tok_s": None if ms_s is None else round(1e3 / ms_s, 1),
                "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
                                    "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
-        if prefill is not None:
-            out["prefill_%d" % args.prompt_tokens] = prefill
+        for pf in prefills:
+            out["prefill_%d" % pf["tokens"]] = pf
         if not args.no_cpu:
             out["cpu_baseline"], out["first_token_matches_cpu"] = run_cpu_decode(path, kv, first_tok, int(toks[0]),
                                                                                 args.cpu_decode_tokens)
@@ -388,6 +388,7 @@ def run_decode(args):
 
 
 PROMPT_T = 512
+PROMPT_TS = (512, 2048)  # prompts the decode leg times by default
 
 
 def prompt_flop(n_layers=32, T=PROMPT_T):
@@ -932,8 +933,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill GEMM leg")
     ap.add_argument("--no-prompt", action="store_true",
                     help="skip the llama_forward prompt on the config-4 model")
-    ap.add_argument("--prompt-tokens", type=int, default=PROMPT_T,
-                    help="tokens of that prompt (default 512; up to the decode model's context)")
+    ap.add_argument("--prompt-tokens", type=int, nargs="+", default=list(PROMPT_TS),
+                    help="tokens of those prompts (default 512 2048; up to the decode model's context)")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
