@@ -130,25 +130,50 @@ hipError_t launch_rope_kv_rows(float* Q, const float* K, const float* V, const f
 }
 
 // ---------------------------------------------------------------------------
-// Keys as fp16 hi/lo rows for the attention's q.k on fp16 matrix cores.
-// Row j of KV head h (keys 0 .. n_keys-1) is scaled by 2^e, e chosen per
-// row so that max|k'| lies in [2^14, 2^15) (e = 0 for an all-zero or
-// non-finite row), and split as hi = rn(k'), lo = rn(k' - hi) (the
-// subtraction is exact in fp32): 22 significant bits of every element within
-// 2^17 of the row maximum, steps of 2^-24 (of k') below that.  With each
-// row goes a flag: the key's V row holds a NaN or an infinity (its P.V terms
-// must then be formed even where e_j = 0, as 0 * v_j is NaN).  Layout: halfs
-// [n_kv][max_seq][hi 0..127 | lo 0..127], then int32 2e + flag [n_kv][max_seq].
-// One 32-lane half of a wave per row, one float4 of K and of V per lane.
+// Keys and values as fp16 hi/lo parts for the attention's matrix-core
+// products (one layer's worth, rebuilt for every prefill chunk).
+//  * Keys: row j of KV head h (keys 0 .. n_keys-1) is scaled by 2^e, e
+//    chosen per row so that max|k'| lies in [2^14, 2^15) (e = 0 for an
+//    all-zero or non-finite row), and split as hi = rn(k'), lo = rn(k' - hi)
+//    (the subtraction is exact in fp32): 22 significant bits of every
+//    element within 2^17 of the row maximum, steps of 2^-24 (of k') below
+//    that.  With each row goes a flag: the key's V row holds a NaN or an
+//    infinity (its P.V terms must then be formed even where e_j = 0, as
+//    0 * v_j is NaN).
+//  * Values: one exponent per KV head, from the largest finite |v| over its
+//    keys (so that max|v'| lies in [2^14, 2^15)), the same hi/lo split, and
+//    stored transposed per 64-key stage, [dim][64 keys], the keys of each
+//    32-key half in the order the P.V fragments read them (positions
+//    8g + 4s + r hold key 16s + 4g + r).
+// Layout (256-byte aligned pieces): K halfs [n_kv][max_seq][hi 128 | lo
+// 128]; int32 2e + flag [n_kv][max_seq]; float partial max|v| [n_kv]
+// [max_seq / 8]; int32 V exponent [n_kv]; V halfs [n_kv][stages][hi | lo]
+// [128][64].
 // ---------------------------------------------------------------------------
-size_t prefill_khl_bytes(uint32_t n_kv, uint32_t max_seq) {
+struct KhlLayout {
+    size_t meta, vmax, vexp, vt, bytes;
+    uint32_t n_wa, n_st;  // partials per head (8 keys each), 64-key stages per head
+};
+
+__host__ __device__ inline KhlLayout khl_layout(uint32_t n_kv, uint32_t max_seq) {
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    KhlLayout L;
     const size_t rows = (size_t)n_kv * max_seq;
-    return ((rows * 2 * kPHd * 2 + 255) & ~(size_t)255) + rows * 4;
+    L.n_wa = (max_seq + 7) / 8;
+    L.n_st = (max_seq + 63) / 64;
+    L.meta = al(rows * 2 * kPHd * 2);
+    L.vmax = L.meta + al(rows * 4);
+    L.vexp = L.vmax + al((size_t)n_kv * L.n_wa * 4);
+    L.vt = L.vexp + al((size_t)n_kv * 4);
+    L.bytes = L.vt + (size_t)n_kv * L.n_st * 64 * 2 * kPHd * 2;
+    return L;
 }
 
-__host__ __device__ inline int* khl_meta(void* khl, uint32_t n_kv, uint32_t max_seq) {
-    const size_t rows = (size_t)n_kv * max_seq;
-    return reinterpret_cast<int*>(static_cast<uint8_t*>(khl) + ((rows * 2 * kPHd * 2 + 255) & ~(size_t)255));
+size_t prefill_khl_bytes(uint32_t n_kv, uint32_t max_seq) { return khl_layout(n_kv, max_seq).bytes; }
+
+template <typename T>
+__host__ __device__ inline T* khl_at(void* khl, size_t off) {
+    return reinterpret_cast<T*>(static_cast<uint8_t*>(khl) + off);
 }
 
 // Exponent e with max|x * 2^e| in [2^14, 2^15) for a finite m = max|x| > 0,
@@ -157,18 +182,34 @@ __device__ __forceinline__ int split_exp(float m) {
     return (m > 0.0f && m <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
 }
 
+// Key rows, their flags, and each 8-row group's largest finite |v|: one
+// 32-lane half of a wave per row, one float4 of K and of V per lane.
 __global__ __launch_bounds__(256) void k_prefill_khl(const float* __restrict__ kv, uint32_t n_keys, uint32_t max_seq,
-                                                     _Float16* __restrict__ khl, int* __restrict__ meta) {
+                                                     void* __restrict__ khl, KhlLayout L) {
+    __shared__ float red[4];
     const uint32_t kvh = blockIdx.y;
     const uint32_t j = blockIdx.x * 8u + (threadIdx.x >> 5), c = threadIdx.x & 31u;
-    if (j >= n_keys) return;  // uniform over the row's 32 lanes
-    const size_t row = (size_t)kvh * max_seq + j;
-    const float4 x = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + 4 * c);
-    const float4 vx = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + kPHd + 4 * c);
-    const bool vbad = !(fabsf(vx.x) <= FLT_MAX && fabsf(vx.y) <= FLT_MAX && fabsf(vx.z) <= FLT_MAX &&
-                        fabsf(vx.w) <= FLT_MAX);
+    const bool ok = j < n_keys;  // uniform over the row's 32 lanes
+    const size_t row = (size_t)kvh * max_seq + (ok ? j : 0u);
+    float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f), vx = x;
+    if (ok) {
+        x = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + 4 * c);
+        vx = *reinterpret_cast<const float4*>(kv + row * (2 * kPHd) + kPHd + 4 * c);
+    }
+    const float va[4] = {fabsf(vx.x), fabsf(vx.y), fabsf(vx.z), fabsf(vx.w)};
+    bool vbad = false;
+    float mv = 0.0f;  // largest finite |v|
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool fin = va[i] <= FLT_MAX;
+        vbad |= !fin;
+        mv = fin ? fmaxf(mv, va[i]) : mv;
+    }
     const uint64_t vb = __ballot(vbad);
     const bool row_vbad = ((threadIdx.x & 32) ? (uint32_t)(vb >> 32) : (uint32_t)vb) != 0u;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) mv = fmaxf(mv, __shfl_xor(mv, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mv;
     float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
     if (!(x.x == x.x && x.y == x.y && x.z == x.z && x.w == x.w)) m = INFINITY;  // NaN: no scaling
 #pragma unroll
@@ -181,15 +222,73 @@ __global__ __launch_bounds__(256) void k_prefill_khl(const float* __restrict__ k
         hi[i] = (_Float16)v[i];
         lo[i] = (_Float16)(v[i] - (float)hi[i]);
     }
-    _Float16* dst = khl + row * (2 * kPHd) + 4 * c;
-    *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(hi);
-    *reinterpret_cast<uint2*>(dst + kPHd) = *reinterpret_cast<const uint2*>(lo);
-    if (c == 0) meta[row] = 2 * e + (row_vbad ? 1 : 0);
+    if (ok) {
+        _Float16* dst = khl_at<_Float16>(khl, 0) + row * (2 * kPHd) + 4 * c;
+        *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(hi);
+        *reinterpret_cast<uint2*>(dst + kPHd) = *reinterpret_cast<const uint2*>(lo);
+        if (c == 0) khl_at<int>(khl, L.meta)[row] = 2 * e + (row_vbad ? 1 : 0);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        khl_at<float>(khl, L.vmax)[(size_t)kvh * L.n_wa + blockIdx.x] =
+            fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Position of key r (0..63) of a stage in the transposed V rows.
+__device__ __forceinline__ uint32_t vt_pos(uint32_t r) {
+    const uint32_t k = r & 31u;
+    return (r & 32u) + 8u * ((k >> 2) & 3u) + 4u * (k >> 4) + (k & 3u);
+}
+
+// V of one 64-key stage of one KV head, scaled by the head's exponent,
+// split into hi/lo and transposed (through LDS); keys past n_keys are 0.
+__global__ __launch_bounds__(256) void k_prefill_vt(const float* __restrict__ kv, uint32_t n_keys, uint32_t max_seq,
+                                                    void* __restrict__ khl, KhlLayout L) {
+    __shared__ float red[4];
+    __shared__ __attribute__((aligned(16))) _Float16 lt[2][kPHd][64 + 8];
+    const uint32_t st = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    // The head's largest finite |v| from k_prefill_khl's partials (exact, so
+    // any order): every workgroup of the head gets the same exponent.
+    const float* vm = khl_at<float>(khl, L.vmax) + (size_t)kvh * L.n_wa;
+    const uint32_t nw = (n_keys + 7) / 8;
+    float m = 0.0f;
+    for (uint32_t i = tid; i < nw; i += 256) m = fmaxf(m, vm[i]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const int ev = split_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    if (st == 0 && tid == 0) khl_at<int>(khl, L.vexp)[kvh] = ev;
+    const float* vbase = kv + (size_t)kvh * max_seq * 2 * kPHd + kPHd;
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t i = tid + 256u * u, r = i >> 5, c = i & 31u;
+        const uint32_t j = st * 64u + r;
+        float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (j < n_keys) x = *reinterpret_cast<const float4*>(vbase + (size_t)j * 2 * kPHd + 4 * c);
+        const float xs[4] = {x.x, x.y, x.z, x.w};
+        const uint32_t pos = vt_pos(r);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = ldexpf(xs[e], ev);
+            const _Float16 hv = (_Float16)v;
+            lt[0][4 * c + e][pos] = hv;
+            lt[1][4 * c + e][pos] = (_Float16)(v - (float)hv);
+        }
+    }
+    __syncthreads();
+    _Float16* dst = khl_at<_Float16>(khl, L.vt) + ((size_t)kvh * L.n_st + st) * (2 * kPHd * 64);
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t q = tid + 256u * u, part = q >> 10, d = (q >> 3) & 127u, k8 = q & 7u;
+        *reinterpret_cast<uint4*>(dst + ((size_t)part * kPHd + d) * 64 + 8 * k8) =
+            *reinterpret_cast<const uint4*>(&lt[part][d][8 * k8]);
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Causal prefill attention: q.k on fp16 matrix cores (v_mfma_f32_16x16x32_f16
-// on hi/lo parts), P.V on v_mfma_f32_16x16x4_f32.
+// Causal prefill attention: q.k and P.V on fp16 matrix cores
+// (v_mfma_f32_16x16x32_f16 on hi/lo parts).
 //
 // Workgroup: 16 queries (a query tile) x HG of the G query heads of one KV
 // head, two waves per head, each taking half of every staged 64-key block (so
@@ -209,6 +308,9 @@ __global__ __launch_bounds__(256) void k_prefill_khl(const float* __restrict__ k
 // exponent from its own 128 elements), and each dot is
 // (hi.hi) + (hi.lo + lo.hi) over the scaled parts (the lo.lo term, at most
 // 2^-22 of |q||k| per element, is left out), times 2^-(e_q + e_k), exact.
+// P.V: e_j (at most 1 for finite scores; the reference's exp gives 91.4 for
+// a NaN) times 2^9, split the same way, against the head's scaled V parts
+// (k_prefill_vt): hi.hi + hi.lo + lo.hi, times 2^-(9 + e_v) at the end.
 //
 // Fragment layouts (D[4*(l/16)+r][l%16] lands in register r of lane l):
 //  * scores S^T[key][query] = K . Q^T on 16x16x32 f16 (lane l feeds 8
@@ -217,13 +319,13 @@ __global__ __launch_bounds__(256) void k_prefill_khl(const float* __restrict__ k
 //    32g + 8c + i of the head (any pairing of the 128 elements works when A
 //    and B agree), so each lane reads 32 consecutive halfs of one key row's
 //    hi and lo parts and keeps 32 consecutive elements of its query;
-//  * P.V on 16x16x4 f32 (lane l feeds A[l%16][l/16] and B[l/16][l%16]):
-//    the scores give lane l query l%16 and keys 4g + r of the 16-key
-//    block, which is exactly lane l's A fragment of O = P . V for step kk = r
-//    if step kk pairs lane group g with key 4g + kk; V is read in that key
-//    order, and output column d of tile t in lane l%16 is 4*(l%16) + t
-//    (t < 4) or 64 + 4*(l%16) + t - 4, so every lane reads and writes
-//    float4s.
+//  * P.V on 16x16x32 f16, one MFMA step per 32 keys (a wave's half of a
+//    staged block): the scores give lane l query l%16 and keys 4g + r of
+//    each 16-key block, so its A row (query l%16) takes slots 8g .. 8g+3
+//    from the first block and 8g+4 .. 8g+7 from the second; the transposed
+//    V rows hold the keys in that slot order, so B column c of tile n
+//    (dimension 16n + c) is one 16-byte read per part, and register r of
+//    lane l holds query 4g + r, dimension 16n + l%16.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
@@ -234,9 +336,11 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     constexpr uint32_t NT = 128 * HG;
     constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
     static_assert(kLoads * NT == kAttnKS * (kPHd / 4), "stage/thread mismatch");
-    static_assert(HG * 64 * 32 <= 2 * kAttnKS * kAttnRS, "the P.V exchange reuses the staging space");
-    // [0]: key rows as fp16 hi (bytes 0..255) and lo (256..511); [1]: V rows
-    __shared__ __attribute__((aligned(16))) float lkv[2][kAttnKS][kAttnRS];
+    static_assert(HG * 64 * 32 <= kAttnKS * kAttnRS, "the P.V exchange reuses the key staging space");
+    // key rows as fp16 hi (bytes 0..255) and lo (256..511)
+    __shared__ __attribute__((aligned(16))) float lk[kAttnKS][kAttnRS];
+    // V of the staged keys, transposed: [hi | lo][dimension][key position]
+    __shared__ __attribute__((aligned(16))) _Float16 lvt[2][kPHd][kAttnKS + 8];
     __shared__ __attribute__((aligned(16))) int lke[kAttnKS];  // the staged keys' exponents
     __shared__ int lvb[kAttnKS];                              // and their V rows' non-finite flags
     __shared__ float xmax[2][HG][16], xsum[HG][16];
@@ -256,10 +360,13 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     const uint32_t n_keys = a.pos0 + t_last + 1u;  // keys of the tile's last query
     const uint32_t n_stages = (n_keys + kAttnKS - 1) / kAttnKS;
     const size_t q_ld = (size_t)a.n_heads * kPHd;
-    const float* kbase = a.kv + (size_t)kvh * a.max_seq * 2 * kPHd;
-    // key rows (hi|lo halfs, 128 floats' worth each) and exponents
-    const float* khbase = reinterpret_cast<const float*>(a.khl) + (size_t)kvh * a.max_seq * kPHd;
-    const int* kmbase = khl_meta(a.khl, a.n_kv, a.max_seq) + (size_t)kvh * a.max_seq;
+    const KhlLayout L = khl_layout(a.n_kv, a.max_seq);
+    // key rows (hi|lo halfs, 128 floats' worth each), 2e + V flag, the
+    // transposed V stages and the head's V exponent
+    const float* khbase = khl_at<const float>(a.khl, 0) + (size_t)kvh * a.max_seq * kPHd;
+    const int* kmbase = khl_at<const int>(a.khl, L.meta) + (size_t)kvh * a.max_seq;
+    const float* vtbase = khl_at<const float>(a.khl, L.vt) + (size_t)kvh * L.n_st * (kPHd * 64);
+    const int ev = khl_at<const int>(a.khl, L.vexp)[kvh];
 
     // This lane's query (B column li) and its 32 elements 32*lg .. 32*lg+31.
     const uint32_t my_t = t0 + li;
@@ -327,7 +434,6 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
             uint32_t j = st * kAttnKS + r;
             j = j < n_keys ? j : n_keys - 1u;
-            const float4* src = reinterpret_cast<const float4*>(kbase + (size_t)j * 2 * kPHd) + c;
             if constexpr (with_k) {
                 // 16 bytes of the key's hi|lo row, moved as raw bits
                 const float4 k4 = reinterpret_cast<const float4*>(khbase + (size_t)j * kPHd)[c];
@@ -338,7 +444,8 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
             }
             if (c == 0) km[u] = kmbase[j];
             if constexpr (with_v) {
-                const float4 v4 = src[kPHd / 4];
+                // 16 bytes (chunk i) of the stage's transposed V parts, raw bits
+                const float4 v4 = reinterpret_cast<const float4*>(vtbase + (size_t)st * (kPHd * 64))[i];
                 vr[4 * u] = v4.x;
                 vr[4 * u + 1] = v4.y;
                 vr[4 * u + 2] = v4.z;
@@ -354,15 +461,17 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
             const uint32_t i = threadIdx.x + u * NT;
             const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
             if constexpr (with_k) {
-                *reinterpret_cast<float4*>(&lkv[0][r][4 * c]) =
+                *reinterpret_cast<float4*>(&lk[r][4 * c]) =
                     make_float4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
                 if (c == 0) lke[r] = km[u] >> 1;
             }
             if constexpr (with_v)
                 if (c == 0) lvb[r] = km[u] & 1;
-            if constexpr (with_v)
-                *reinterpret_cast<float4*>(&lkv[1][r][4 * c]) =
+            if constexpr (with_v) {
+                const uint32_t part = i >> 10, d = (i >> 3) & (kPHd - 1), k8 = i & 7u;
+                *reinterpret_cast<float4*>(&lvt[part][d][8 * k8]) =
                     make_float4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
+            }
         }
     };
 
@@ -371,7 +480,7 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     // their sum, then the exponents undone.
     auto scores = [&](uint32_t sub) -> f4v {
         f4v d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const _Float16* kr = reinterpret_cast<const _Float16*>(&lkv[0][sub * 16 + li][0]) + 32 * lg;
+        const _Float16* kr = reinterpret_cast<const _Float16*>(&lk[sub * 16 + li][0]) + 32 * lg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const h8v kh = *reinterpret_cast<const h8v*>(kr + 8 * c);
@@ -407,41 +516,49 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
         __syncthreads();
         mx = fmaxf(xmax[0][hw][li], xmax[1][hw][li]);
     };
-    // e_j of the 16 keys of d, their sum and P.V with the staged V rows.
+    // e_j of the wave's 32 keys (d0: keys jb .. jb+15, d1: jb+16 .. jb+31),
+    // their sum and P.V with the staged V parts.
     f4v acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     float sum = 0.0f;
-    auto pv_sub = [&](uint32_t sub, uint32_t jb, const f4v& d) {
-        float e[4];
+    auto pv32 = [&](uint32_t jb, const f4v& d0, const f4v& d1) {
+        float e[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t j = jb + 4 * lg + r;
-            const float dd = d[r] * a.scale - mx;
-            float ev = 0.0f;
-            if (q_ok && j <= P) ev = (j < Sv) ? exp_approx(dd) : expf(dd);
-            e[r] = ev;
-            sum += ev;
-        }
-        // A 16-key block whose e_j are 0 for every query of the tile adds
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t j = jb + 16 * s2 + 4 * lg + r;
+                const float dd = (s2 ? d1[r] : d0[r]) * a.scale - mx;
+                float ev_j = 0.0f;
+                if (q_ok && j <= P) ev_j = (j < Sv) ? exp_approx(dd) : expf(dd);
+                e[4 * s2 + r] = ev_j;
+                sum += ev_j;
+            }
+        // A 32-key step whose e_j are 0 for every query of the tile adds
         // exact zeros (0 * v_j for finite v_j): its P.V is skipped.  (The
         // polynomial exp is 0 below about -2.18, so most keys of a peaked
         // score row take no part.)
-        const bool nz = (e[0] != 0.0f) | (e[1] != 0.0f) | (e[2] != 0.0f) | (e[3] != 0.0f);
-        if (__ballot(nz || lvb[sub * 16 + li] != 0) == 0ull) return;  // wave-uniform
+        bool nz = false;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const float* vr = &lkv[1][sub * 16 + 4 * lg + kk][0];
-            const float4 v0 = *reinterpret_cast<const float4*>(vr + 4 * li);
-            const float4 v1 = *reinterpret_cast<const float4*>(vr + 64 + 4 * li);
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.x, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.y, acc[1], 0, 0, 0);
-            acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.z, acc[2], 0, 0, 0);
-            acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v0.w, acc[3], 0, 0, 0);
-            acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.x, acc[4], 0, 0, 0);
-            acc[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.y, acc[5], 0, 0, 0);
-            acc[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.z, acc[6], 0, 0, 0);
-            acc[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(e[kk], v1.w, acc[7], 0, 0, 0);
+        for (int i = 0; i < 8; ++i) nz |= e[i] != 0.0f;
+        const uint32_t kb = 32 * half;  // the wave's keys within the staged block
+        if (__ballot(nz || lvb[kb + li] != 0 || lvb[kb + 16 + li] != 0) == 0ull) return;  // wave-uniform
+        h8v ph, pl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float v = e[i] * 512.0f;
+            const _Float16 hv = (_Float16)v;
+            ph[i] = hv;
+            pl[i] = (_Float16)(v - (float)hv);
+        }
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const h8v vh = *reinterpret_cast<const h8v*>(&lvt[0][16 * n + li][kb + 8 * lg]);
+            const h8v vl = *reinterpret_cast<const h8v*>(&lvt[1][16 * n + li][kb + 8 * lg]);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vh, acc[n], 0, 0, 0);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vl, acc[n], 0, 0, 0);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vh, acc[n], 0, 0, 0);
         }
     };
 
@@ -470,7 +587,7 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
         }
         fetch(0, OnlyV{});  // pass 2's first block, in flight during the exchange
         exchange_max();
-        // ---- pass 2: e_j, their sum and P.V (V rows only staged) ----
+        // ---- pass 2: e_j, their sum and P.V (V parts only staged) ----
 #pragma unroll
         for (uint32_t st = 0; st < kCacheStages; ++st) {
             if (st < n_stages) {
@@ -478,12 +595,8 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
                 put(OnlyV{});
                 __syncthreads();
                 if (st + 1 < n_stages) fetch(st + 1, OnlyV{});
-#pragma unroll
-                for (uint32_t s2 = 0; s2 < 2; ++s2) {
-                    const uint32_t sub = 2 * half + s2;
-                    const uint32_t jb = st * kAttnKS + sub * 16;
-                    if (jb < n_keys) pv_sub(sub, jb, sc[st][s2]);
-                }
+                const uint32_t jb = st * kAttnKS + 32 * half;
+                if (jb < n_keys) pv32(jb, sc[st][0], jb + 16 < n_keys ? sc[st][1] : f4v{0.0f, 0.0f, 0.0f, 0.0f});
             }
         }
     } else {
@@ -510,12 +623,11 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
             put(WithV{});
             __syncthreads();
             if (st + 1 < n_stages) fetch(st + 1, WithV{});
-#pragma unroll
-            for (uint32_t s2 = 0; s2 < 2; ++s2) {
-                const uint32_t sub = 2 * half + s2;
-                const uint32_t jb = st * kAttnKS + sub * 16;
-                if (jb >= n_keys) break;
-                pv_sub(sub, jb, scores(sub));
+            const uint32_t jb = st * kAttnKS + 32 * half;
+            if (jb < n_keys) {
+                const f4v d0 = scores(2 * half);
+                const f4v d1 = jb + 16 < n_keys ? scores(2 * half + 1) : f4v{0.0f, 0.0f, 0.0f, 0.0f};
+                pv32(jb, d0, d1);
             }
         }
     }
@@ -525,7 +637,7 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     // ---- the second half's partials join the first's through LDS (the
     // staging space, free after this barrier) ----
     __syncthreads();
-    float* xo = &lkv[0][0][0] + (size_t)(hw * 64 + lane) * 32;
+    float* xo = &lk[0][0] + (size_t)(hw * 64 + lane) * 32;
     if (half == 1) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) *reinterpret_cast<f4v*>(xo + 4 * t) = acc[t];
@@ -537,7 +649,8 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     for (int t = 0; t < 8; ++t) acc[t] += *reinterpret_cast<const f4v*>(xo + 4 * t);
     sum += xsum[hw][li];
 
-    // ---- output: register r of lane l is query 4*(l/16) + r ----
+    // ---- output: register r of lane l is query 4*(l/16) + r, dimension
+    // 16n + l%16 of tile n; the parts' scales undone exactly first ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint32_t i = 4 * lg + (uint32_t)r;
@@ -546,12 +659,12 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
         if (t < a.T) {
             const bool small = a.pos0 + t + 1u < 8u;
             const float inv = 1.0f / total;
-            float o[8];
+            float* dst = a.o + (size_t)t * q_ld + (size_t)h * kPHd + li;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) o[c] = small ? acc[c][r] / total : acc[c][r] * inv;
-            float* dst = a.o + (size_t)t * q_ld + (size_t)h * kPHd;
-            *reinterpret_cast<float4*>(dst + 4 * li) = make_float4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<float4*>(dst + 64 + 4 * li) = make_float4(o[4], o[5], o[6], o[7]);
+            for (int n = 0; n < 8; ++n) {
+                const float v = ldexpf(acc[n][r], -(9 + ev));
+                dst[16 * n] = small ? v / total : v * inv;
+            }
         }
     }
 }
@@ -560,9 +673,14 @@ template <uint32_t G>
 static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
     constexpr uint32_t HG = G < 2 ? G : 2;  // heads per workgroup
     const uint32_t n_keys = a.pos0 + a.T;
-    hipLaunchKernelGGL(k_prefill_khl, dim3((n_keys + 7) / 8, a.n_kv), dim3(256), 0, s, a.kv, n_keys, a.max_seq,
-                       static_cast<_Float16*>(a.khl), khl_meta(a.khl, a.n_kv, a.max_seq));
+    const KhlLayout L = khl_layout(a.n_kv, a.max_seq);
+    hipLaunchKernelGGL(k_prefill_khl, dim3((n_keys + 7) / 8, a.n_kv), dim3(256), 0, s, a.kv, n_keys, a.max_seq, a.khl,
+                       L);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_prefill_vt, dim3((n_keys + 63) / 64, a.n_kv), dim3(256), 0, s, a.kv, n_keys, a.max_seq,
+                       a.khl, L);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t n_qt = (a.T + 15) / 16;
     hipLaunchKernelGGL((k_prefill_attn<G, HG>), dim3(n_qt, a.n_kv * (G / HG)), dim3(128 * HG), 0, s, a);
