@@ -404,7 +404,7 @@ def prompt_flop(n_layers=32, T=PROMPT_T):
 
 def run_prompt(m, h, T=PROMPT_T, reps=3):
     """llama_forward of a T-token prompt (512 by default) at position 0 on
-    the 32-layer model (the batched prefill, in chunks of up to 512 tokens),
+    the 32-layer model (the batched prefill, in chunks of up to 2048 tokens),
     wall clock around the synchronous call."""
     if T < 1 or T > h.max_seq:
         raise SystemExit(f"bench.py: --prompt-tokens must be 1..{h.max_seq}")

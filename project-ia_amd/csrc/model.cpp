@@ -755,7 +755,7 @@ q_error_code llama_build_graph(q_context* __restrict__ ctx, q_llama_model* __res
     }
     // Everything a later call needs is allocated here, so no llama_forward
     // (one token or a prompt) and no device generation loop allocates: the
-    // prefill rows and GEMM workspace for chunks of up to 512 tokens and the
+    // prefill rows and GEMM workspace for chunks of up to 2048 tokens and the
     // sampler's workspace.
     q_error_code rc = prefill_alloc(p);
     if (rc == Q_OK) {
@@ -788,7 +788,7 @@ void llama_free_graph(q_llama_model* __restrict__ model) {
 // Reference src/models/model.c:1655-1850: tokens[0..seq_len) at positions
 // pos.., logits of the last token copied to the host buffer `logits`, the KV
 // cache filled at pos .. pos+seq_len-1.  One token runs the captured decode
-// step; more run the batched prefill in chunks of up to 512 tokens (the
+// step; more run the batched prefill in chunks of up to 2048 tokens (the
 // result of one decode step per token: causal attention over the cache).
 q_error_code llama_forward(q_llama_model* __restrict__ model, q_context* __restrict__ ctx,
                            const uint32_t* __restrict__ tokens, uint32_t seq_len, uint32_t pos,
