@@ -424,7 +424,7 @@ def run_prompt(m, h, T=PROMPT_T, reps=3):
             "frac_of_fp16_mfma_peak": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "workload": "llama_forward(%d tokens, pos 0) on the config-4 model (32 layers, Llama-3-8B shape, "
                         "Q4_0; chunks of up to 2048 tokens): every projection an MFMA GEMM, causal attention with "
-                        "q.k on fp16 hi/lo MFMA and P.V on fp32 MFMA, KV rows 0..%d "
+                        "q.k and P.V on fp16 hi/lo MFMA, KV rows 0..%d "
                         "written, LM head of the last token; wall clock of the synchronous call incl. the "
                         "token upload and the 513 KB logits download" % (T, T - 1)}
 
