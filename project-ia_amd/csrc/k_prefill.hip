@@ -294,9 +294,11 @@ __global__ __launch_bounds__(256) void k_prefill_vt(const float* __restrict__ kv
 // head, two waves per head, each taking half of every staged 64-key block (so
 // a tile's serial chain is half its keys); the 2HG waves share the key/value
 // rows, staged in LDS 64 keys at a time, the next block's rows loading into
-// registers while the current one is used.  G/HG workgroups share a (query
-// tile, KV head): more, smaller workgroups even out the causal triangle's
-// unequal tiles over the CUs.  Per query (as in the decode step):
+// registers while the current one is used.  HG = min(G, 4): a GQA group of
+// up to 4 heads shares one staging of its keys and values (8 waves, one
+// workgroup per CU); G = 8 takes two workgroups per (query tile, KV head).
+// Workgroups start longest tile first (see the grid order below).  Per
+// query (as in the decode step):
 // s_j = (q . k_j) * scale for j <= P (its position), m = max_j s_j,
 // e_j = exp_approx(s_j - m) for j < (P+1) & ~7 and expf above (all expf when
 // P+1 < 8), o = sum_j e_j v_j times 1/sum_j e_j (divided by the sum when
@@ -331,7 +333,7 @@ constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
 
 template <uint32_t G, uint32_t HG>
-__global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) void k_prefill_attn(const PrefillAttnArgs a) {
+__global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2 ? HG : 2))) void k_prefill_attn(const PrefillAttnArgs a) {
     static_assert(G % HG == 0, "head split");
     constexpr uint32_t NT = 128 * HG;
     constexpr uint32_t kLoads = kAttnKS * (kPHd / 4) / NT;  // float4 per thread per staged matrix
@@ -346,11 +348,12 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
     __shared__ float xmax[2][HG][16], xsum[HG][16];
 
     const uint32_t n_qt = (a.T + 15) / 16;
-    // The first half of the grid takes the longest rows first, the second
-    // half the shortest first: a CU that holds workgroups b and b + half the
-    // grid then gets about the same number of keys as any other.
-    const uint32_t qt = (2 * blockIdx.y < gridDim.y) ? n_qt - 1 - blockIdx.x : blockIdx.x;
-    const uint32_t kvh = blockIdx.y / (G / HG), hs = blockIdx.y % (G / HG);
+    // Longest query tiles first: the grid's y runs over the query tiles from
+    // the last (most keys) down, x over the KV heads and head groups, so
+    // workgroups start in order of decreasing work and the short tiles fill
+    // the last rounds.
+    const uint32_t qt = n_qt - 1 - blockIdx.y;
+    const uint32_t kvh = blockIdx.x / (G / HG), hs = blockIdx.x % (G / HG);
     const uint32_t t0 = qt * 16;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t hw = wave % HG, half = wave / HG;  // head within the workgroup, half of each block
@@ -671,7 +674,7 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG))) 
 
 template <uint32_t G>
 static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
-    constexpr uint32_t HG = G < 2 ? G : 2;  // heads per workgroup
+    constexpr uint32_t HG = G < 4 ? G : 4;  // heads per workgroup
     const uint32_t n_keys = a.pos0 + a.T;
     const KhlLayout L = khl_layout(a.n_kv, a.max_seq);
     hipLaunchKernelGGL(k_prefill_khl, dim3((n_keys + 7) / 8, a.n_kv), dim3(256), 0, s, a.kv, n_keys, a.max_seq, a.khl,
@@ -683,7 +686,7 @@ static hipError_t run_prefill_attention(const PrefillAttnArgs& a, hipStream_t s)
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t n_qt = (a.T + 15) / 16;
-    hipLaunchKernelGGL((k_prefill_attn<G, HG>), dim3(n_qt, a.n_kv * (G / HG)), dim3(128 * HG), 0, s, a);
+    hipLaunchKernelGGL((k_prefill_attn<G, HG>), dim3(a.n_kv * (G / HG), n_qt), dim3(128 * HG), 0, s, a);
     return hipGetLastError();
 }
 
