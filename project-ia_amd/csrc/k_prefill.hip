@@ -330,6 +330,8 @@ __global__ __launch_bounds__(256) void k_prefill_vt(const float* __restrict__ kv
 //    lane l holds query 4g + r, dimension 16n + l%16.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kAttnKS = 64;         // keys per LDS stage
+constexpr int kAttnBufFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family): out of range reads 0
+typedef uint32_t u4v_a __attribute__((ext_vector_type(4)));
 constexpr uint32_t kAttnRS = kPHd + 4;   // padded LDS row (floats)
 
 template <uint32_t G, uint32_t HG>
@@ -377,6 +379,11 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
     const uint32_t P = a.pos0 + my_t;  // attends keys 0..P
     const uint32_t S = P + 1u;
     const uint32_t Sv = S >= 8u ? (S & ~7u) : 0u;
+    // Keys below `inner` are attended by every query of the tile, all on the
+    // polynomial exp (a full tile: the first query's Sv; 0 for a partial
+    // last tile): steps of 32 keys below it need no masks.
+    const uint32_t S_first = a.pos0 + t0 + 1u;
+    const uint32_t inner = (t0 + 16u <= a.T && S_first >= 8u) ? (S_first & ~7u) : 0u;
     // Its scaled hi/lo parts, step c holding elements 32*lg + 8c .. +7, and
     // its exponent (the max over the 4 lanes that hold the query).
     h8v qh[4], ql[4];
@@ -416,8 +423,10 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
     }
 
     // Rows st*KS .. +KS-1 of K (and V): fetch into registers, then put into
-    // LDS; rows past the tile's keys repeat its last key (in bounds; masked
-    // by j <= P below).
+    // LDS.  The loads go through buffer resources that end at the tile's
+    // last key (rows past it read zeros, masked by j <= P below), with
+    // per-lane offsets fixed for the whole kernel and the stage as a scalar
+    // offset, so a fetch costs no address arithmetic.
     // (vectors rather than arrays: arrays live across the loop stayed in
     // scratch memory)
     typedef float stage_v __attribute__((ext_vector_type(4 * kLoads)));
@@ -428,31 +437,38 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
     using NoV = std::integral_constant<int, 0>;
     using WithV = std::integral_constant<int, 1>;
     using OnlyV = std::integral_constant<int, 2>;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)khbase, 0, (int)(n_keys * kPHd * 4u), kAttnBufFlags);
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kmbase, 0, (int)(n_keys * 4u), kAttnBufFlags);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vtbase, 0, (int)(n_stages * kPHd * 64u * 4u), kAttnBufFlags);
+    // Chunk i = threadIdx.x + u*NT of a stage is bytes 16i.. of its K rows
+    // (row i/32) and of its V parts alike: one lane offset, the rest scalar.
+    const uint32_t lane_off = threadIdx.x * 16u, lane_row = (threadIdx.x / (kPHd / 4)) * 4u;
     auto fetch = [&](uint32_t st, auto modec) {
         constexpr int mode = decltype(modec)::value;
         constexpr bool with_k = mode != 2, with_v = mode != 0;
 #pragma unroll
         for (uint32_t u = 0; u < kLoads; ++u) {
-            const uint32_t i = threadIdx.x + u * NT;
-            const uint32_t r = i / (kPHd / 4), c = i % (kPHd / 4);
-            uint32_t j = st * kAttnKS + r;
-            j = j < n_keys ? j : n_keys - 1u;
+            const uint32_t so = st * (kAttnKS * kPHd * 4u) + u * NT * 16u;  // == st * 32 KB + u * NT * 16
             if constexpr (with_k) {
                 // 16 bytes of the key's hi|lo row, moved as raw bits
-                const float4 k4 = reinterpret_cast<const float4*>(khbase + (size_t)j * kPHd)[c];
-                kr[4 * u] = k4.x;
-                kr[4 * u + 1] = k4.y;
-                kr[4 * u + 2] = k4.z;
-                kr[4 * u + 3] = k4.w;
+                const u4v_a k4 = __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off, so, 0);
+                kr[4 * u] = __uint_as_float(k4[0]);
+                kr[4 * u + 1] = __uint_as_float(k4[1]);
+                kr[4 * u + 2] = __uint_as_float(k4[2]);
+                kr[4 * u + 3] = __uint_as_float(k4[3]);
             }
-            if (c == 0) km[u] = kmbase[j];
+            // every lane of the row's 32 loads its 2e + V flag (one address)
+            km[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rm, lane_row, st * (kAttnKS * 4u) + u * (NT / 8u), 0);
             if constexpr (with_v) {
                 // 16 bytes (chunk i) of the stage's transposed V parts, raw bits
-                const float4 v4 = reinterpret_cast<const float4*>(vtbase + (size_t)st * (kPHd * 64))[i];
-                vr[4 * u] = v4.x;
-                vr[4 * u + 1] = v4.y;
-                vr[4 * u + 2] = v4.z;
-                vr[4 * u + 3] = v4.w;
+                const u4v_a v4 = __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off, so, 0);
+                vr[4 * u] = __uint_as_float(v4[0]);
+                vr[4 * u + 1] = __uint_as_float(v4[1]);
+                vr[4 * u + 2] = __uint_as_float(v4[2]);
+                vr[4 * u + 3] = __uint_as_float(v4[3]);
             }
         }
     };
@@ -478,32 +494,50 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
         }
     };
 
-    // Scores of keys sub*16 .. sub*16+15 of the staged block (times scale
-    // applied by the caller): hi.hi and the two cross terms in two chains,
-    // their sum, then the exponents undone.
-    auto scores = [&](uint32_t sub) -> f4v {
-        f4v d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const _Float16* kr = reinterpret_cast<const _Float16*>(&lk[sub * 16 + li][0]) + 32 * lg;
+    // Scores of keys sub*16 .. sub*16+31 of the staged block (the wave's 32
+    // keys; times scale applied by the caller), r0 for the first 16, r1 for
+    // the next: per 16 keys hi.hi and the two cross terms in two chains,
+    // their sum, then the exponents undone.  The two 16-key products run
+    // interleaved (four independent MFMA chains).
+    auto scores2 = [&](uint32_t sub, f4v& r0, f4v& r1) {
+        f4v a0 = {0.0f, 0.0f, 0.0f, 0.0f}, b0 = a0, a1 = a0, b1 = a0;
+        const _Float16* k0 = reinterpret_cast<const _Float16*>(&lk[sub * 16 + li][0]) + 32 * lg;
+        const _Float16* k1 = reinterpret_cast<const _Float16*>(&lk[sub * 16 + 16 + li][0]) + 32 * lg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const h8v kh = *reinterpret_cast<const h8v*>(kr + 8 * c);
-            const h8v kl = *reinterpret_cast<const h8v*>(kr + kPHd + 8 * c);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], d1, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], d1, 0, 0, 0);
+            const h8v kh0 = *reinterpret_cast<const h8v*>(k0 + 8 * c);
+            const h8v kl0 = *reinterpret_cast<const h8v*>(k0 + kPHd + 8 * c);
+            const h8v kh1 = *reinterpret_cast<const h8v*>(k1 + 8 * c);
+            const h8v kl1 = *reinterpret_cast<const h8v*>(k1 + kPHd + 8 * c);
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qh[c], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qh[c], a1, 0, 0, 0);
+            b0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, ql[c], b0, 0, 0, 0);
+            b1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, ql[c], b1, 0, 0, 0);
+            b0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qh[c], b0, 0, 0, 0);
+            b1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qh[c], b1, 0, 0, 0);
         }
-        f4v d = d0 + d1;
-        const int4 ek = *reinterpret_cast<const int4*>(&lke[sub * 16 + 4 * lg]);
-        d[0] = ldexpf(d[0], -(eq + ek.x));
-        d[1] = ldexpf(d[1], -(eq + ek.y));
-        d[2] = ldexpf(d[2], -(eq + ek.z));
-        d[3] = ldexpf(d[3], -(eq + ek.w));
-        return d;
+        r0 = a0 + b0;
+        r1 = a1 + b1;
+        const int4 e0 = *reinterpret_cast<const int4*>(&lke[sub * 16 + 4 * lg]);
+        const int4 e1 = *reinterpret_cast<const int4*>(&lke[sub * 16 + 16 + 4 * lg]);
+        r0[0] = ldexpf(r0[0], -(eq + e0.x));
+        r0[1] = ldexpf(r0[1], -(eq + e0.y));
+        r0[2] = ldexpf(r0[2], -(eq + e0.z));
+        r0[3] = ldexpf(r0[3], -(eq + e0.w));
+        r1[0] = ldexpf(r1[0], -(eq + e1.x));
+        r1[1] = ldexpf(r1[1], -(eq + e1.y));
+        r1[2] = ldexpf(r1[2], -(eq + e1.z));
+        r1[3] = ldexpf(r1[3], -(eq + e1.w));
     };
 
     // Row max over the 16 keys of d (scores of keys jb .. jb+15).
     float mx = -INFINITY;
     auto max_sub = [&](uint32_t jb, const f4v& d) {
+        if (jb + 16u <= inner) {  // wave-uniform: every key attended
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, d[r] * a.scale);
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t j = jb + 4 * lg + r;
@@ -527,24 +561,35 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
     float sum = 0.0f;
     auto pv32 = [&](uint32_t jb, const f4v& d0, const f4v& d1) {
         float e[8];
+        if (jb + 32u <= inner) {
+            // wave-uniform: every key attended, on the polynomial exp (its
+            // argument s_j - m is <= 0 or NaN: exp_approx_nonpos)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t j = jb + 16 * s2 + 4 * lg + r;
-                const float dd = (s2 ? d1[r] : d0[r]) * a.scale - mx;
-                float ev_j = 0.0f;
-                if (q_ok && j <= P) ev_j = (j < Sv) ? exp_approx(dd) : expf(dd);
-                e[4 * s2 + r] = ev_j;
-                sum += ev_j;
-            }
+                for (int r = 0; r < 4; ++r) e[4 * s2 + r] = exp_approx_nonpos((s2 ? d1[r] : d0[r]) * a.scale - mx);
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t j = jb + 16 * s2 + 4 * lg + r;
+                    const float dd = (s2 ? d1[r] : d0[r]) * a.scale - mx;
+                    float ev_j = 0.0f;
+                    if (q_ok && j <= P) ev_j = (j < Sv) ? exp_approx(dd) : expf(dd);
+                    e[4 * s2 + r] = ev_j;
+                }
+        }
+        // The step's 8 values summed as a tree, then added to the row sum;
+        // e_j >= 0 (or NaN), so the step's values are all 0 exactly when
+        // their sum is.
+        const float es = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+        sum += es;
         // A 32-key step whose e_j are 0 for every query of the tile adds
         // exact zeros (0 * v_j for finite v_j): its P.V is skipped.  (The
         // polynomial exp is 0 below about -2.18, so most keys of a peaked
         // score row take no part.)
-        bool nz = false;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) nz |= e[i] != 0.0f;
+        const bool nz = es != 0.0f;
         const uint32_t kb = 32 * half;  // the wave's keys within the staged block
         if (__ballot(nz || lvb[kb + li] != 0 || lvb[kb + 16 + li] != 0) == 0ull) return;  // wave-uniform
         h8v ph, pl;
@@ -555,13 +600,23 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
             ph[i] = hv;
             pl[i] = (_Float16)(v - (float)hv);
         }
+        // Four dimension tiles at a time: their 8 fragment reads first, then
+        // the three products of each tile in turn across the four (the
+        // same order per tile, four independent chains).
 #pragma unroll
-        for (int n = 0; n < 8; ++n) {
-            const h8v vh = *reinterpret_cast<const h8v*>(&lvt[0][16 * n + li][kb + 8 * lg]);
-            const h8v vl = *reinterpret_cast<const h8v*>(&lvt[1][16 * n + li][kb + 8 * lg]);
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vh, acc[n], 0, 0, 0);
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vl, acc[n], 0, 0, 0);
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vh, acc[n], 0, 0, 0);
+        for (int n0 = 0; n0 < 8; n0 += 4) {
+            h8v vh[4], vl[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vh[i] = *reinterpret_cast<const h8v*>(&lvt[0][16 * (n0 + i) + li][kb + 8 * lg]);
+                vl[i] = *reinterpret_cast<const h8v*>(&lvt[1][16 * (n0 + i) + li][kb + 8 * lg]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[n0 + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vh[i], acc[n0 + i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[n0 + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vl[i], acc[n0 + i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[n0 + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vh[i], acc[n0 + i], 0, 0, 0);
         }
     };
 
@@ -577,15 +632,11 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
                 put(NoV{});
                 __syncthreads();
                 if (st + 1 < n_stages) fetch(st + 1, NoV{});
-#pragma unroll
-                for (uint32_t s2 = 0; s2 < 2; ++s2) {
-                    const uint32_t sub = 2 * half + s2;
-                    const uint32_t jb = st * kAttnKS + sub * 16;
-                    if (jb < n_keys) {
-                        sc[st][s2] = scores(sub);
-                        max_sub(jb, sc[st][s2]);
-                    }
-                }
+                // (keys past the tile's last are masked by j <= P)
+                const uint32_t jb = st * kAttnKS + 32 * half;
+                scores2(2 * half, sc[st][0], sc[st][1]);
+                max_sub(jb, sc[st][0]);
+                max_sub(jb + 16, sc[st][1]);
             }
         }
         fetch(0, OnlyV{});  // pass 2's first block, in flight during the exchange
@@ -610,13 +661,11 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
             put(NoV{});
             __syncthreads();
             if (st + 1 < n_stages) fetch(st + 1, NoV{});
-#pragma unroll
-            for (uint32_t s2 = 0; s2 < 2; ++s2) {
-                const uint32_t sub = 2 * half + s2;
-                const uint32_t jb = st * kAttnKS + sub * 16;
-                if (jb >= n_keys) break;
-                max_sub(jb, scores(sub));
-            }
+            const uint32_t jb = st * kAttnKS + 32 * half;
+            f4v d0, d1;
+            scores2(2 * half, d0, d1);
+            max_sub(jb, d0);
+            max_sub(jb + 16, d1);
         }
         fetch(0, WithV{});  // pass 2's first block, in flight during the exchange
         exchange_max();
@@ -628,8 +677,9 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
             if (st + 1 < n_stages) fetch(st + 1, WithV{});
             const uint32_t jb = st * kAttnKS + 32 * half;
             if (jb < n_keys) {
-                const f4v d0 = scores(2 * half);
-                const f4v d1 = jb + 16 < n_keys ? scores(2 * half + 1) : f4v{0.0f, 0.0f, 0.0f, 0.0f};
+                f4v d0, d1;
+                scores2(2 * half, d0, d1);
+                if (jb + 16 >= n_keys) d1 = f4v{0.0f, 0.0f, 0.0f, 0.0f};
                 pv32(jb, d0, d1);
             }
         }

@@ -29,6 +29,22 @@ __device__ __forceinline__ float exp_approx(float x) {
     return r;
 }
 
+// exp_approx for x <= 0 or NaN (a softmax argument s - max s), the same
+// values without the +-10 flags: x <= -10 already gives 0 (t clamps to -5,
+// where the polynomial is -12.33, and max(r, 0) is 0) and x > 10 cannot
+// occur; a NaN takes t = 5 in both (91.41).
+__device__ __forceinline__ float exp_approx_nonpos(float x) {
+    float t = (x < 5.0f) ? x : 5.0f;
+    t = (t > -5.0f) ? t : -5.0f;
+    float r = 0.00833333f;
+    r = fmaf(r, t, 0.04166667f);
+    r = fmaf(r, t, 0.16666667f);
+    r = fmaf(r, t, 0.5f);
+    r = fmaf(r, t, 1.0f);
+    r = fmaf(r, t, 1.0f);
+    return (r > 0.0f) ? r : 0.0f;
+}
+
 // SiLU of reference src/ops/avx2/silu.c:75-82 (vector part).
 __device__ __forceinline__ float silu_approx(float x) {
     const float e = exp_approx(-x);
