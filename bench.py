@@ -328,6 +328,37 @@ def scratch_dir(need_bytes):
     raise SystemExit("bench.py: no scratch space for the synthetic model")
 
 
+def graph_node_floor_us(n_nodes=200):
+    """Replay time per node of a captured graph of n_nodes back-to-back
+    one-workgroup launches (qh_add_f32 over 64 floats, each reading the
+    previous one's output): the fixed cost every node of a decode graph
+    pays, whatever its work."""
+    import qorus_amd as qa
+    lib = qa.lib()
+    a = qa.DeviceBuffer.from_numpy(np.ones(64, np.float32))
+    b = qa.DeviceBuffer.from_numpy(np.zeros(64, np.float32))
+    stream = qa.Stream()
+    s = stream.handle
+    qa.check(lib.qh_stream_begin_capture(s), "begin_capture")
+    for i in range(n_nodes):
+        src, dst = (a, b) if i % 2 == 0 else (b, a)
+        qa.check(lib.qh_add_f32(src.ptr, src.ptr, dst.ptr, 64, s), "add")
+    g = C.c_void_p()
+    qa.check(lib.qh_stream_end_capture(s, C.byref(g)), "end_capture")
+    qa.check(lib.qh_graph_launch(g.value, s))  # warm
+    best = None
+    for _ in range(3):
+        e0, e1 = qa.Event(), qa.Event()
+        e0.record(stream)
+        qa.check(lib.qh_graph_launch(g.value, s))
+        e1.record(stream)
+        stream.sync()
+        ms = e0.elapsed_ms(e1)
+        best = ms if best is None else min(best, ms)
+    lib.qh_graph_destroy(g.value)
+    return round(best * 1e3 / n_nodes, 3)
+
+
 def run_decode(args):
     import shutil
     import qorus_amd as qa
@@ -377,6 +408,10 @@ def run_decode(args):
                "sampled_tok_s": None if ms_s is None else round(1e3 / ms_s, 1),
                "sampled_workload": "same steps, each token drawn on the device by q_sample_token's pipeline "
                                    "(temperature 0.8, top-k 40, top-p 0.95); only the tokens leave the GPU"}
+        out["graph_node_floor_us"] = graph_node_floor_us()
+        out["graph_node_floor_workload"] = ("replay time per node of a captured graph of 200 back-to-back "
+                                            "one-workgroup qh_add_f32 launches: the fixed cost of every node "
+                                            "of the decode graph (7 per layer, 3 per token besides)")
         for pf in prefills:
             out["prefill_%d" % pf["tokens"]] = pf
         if not args.no_cpu:
