@@ -11,8 +11,9 @@ namespace qh {
 // Polynomial exp of reference src/ops/avx2/avx_math.h:10-61, bit-exact:
 // flags on the unclamped x (ordered compares), clamp with x86 minps/maxps
 // semantics ((a<b)?a:b, (a>b)?a:b), degree-5 Horner in fmaf, max(r,0),
-// x < -10 -> 0, x > 10 -> 22026.
-__device__ __forceinline__ float exp_approx(float x) {
+// x < -10 -> 0, x > 10 -> 22026.  (Host-callable too, for the exhaustive
+// host check of the two forms below.)
+__host__ __device__ __forceinline__ float exp_approx(float x) {
     const bool very_neg = x < -10.0f;
     const bool very_pos = x > 10.0f;
     float t = (x < 5.0f) ? x : 5.0f;
@@ -33,7 +34,7 @@ __device__ __forceinline__ float exp_approx(float x) {
 // values without the +-10 flags: x <= -10 already gives 0 (t clamps to -5,
 // where the polynomial is -12.33, and max(r, 0) is 0) and x > 10 cannot
 // occur; a NaN takes t = 5 in both (91.41).
-__device__ __forceinline__ float exp_approx_nonpos(float x) {
+__host__ __device__ __forceinline__ float exp_approx_nonpos(float x) {
     float t = (x < 5.0f) ? x : 5.0f;
     t = (t > -5.0f) ? t : -5.0f;
     float r = 0.00833333f;
