@@ -423,10 +423,14 @@ __global__ __launch_bounds__(128 * HG) __attribute__((amdgpu_waves_per_eu(HG < 2
     }
 
     // Rows st*KS .. +KS-1 of K (and V): fetch into registers, then put into
-    // LDS.  The loads go through buffer resources that end at the tile's
-    // last key (rows past it read zeros, masked by j <= P below), with
-    // per-lane offsets fixed for the whole kernel and the stage as a scalar
-    // offset, so a fetch costs no address arithmetic.
+    // LDS.  The loads go through buffer resources with per-lane offsets
+    // fixed for the whole kernel and the stage as a scalar offset, so a
+    // fetch costs no address arithmetic.  The K and exponent resources end
+    // at the tile's last key: a valid row's lane offset always lies inside,
+    // and rows past the last key (zeros, or the rows behind them in the same
+    // workspace, whether or not the hardware range check counts the scalar
+    // offset) only meet scores masked by j <= P below and the zero V parts
+    // k_prefill_vt writes past the keys.
     // (vectors rather than arrays: arrays live across the loop stayed in
     // scratch memory)
     typedef float stage_v __attribute__((ext_vector_type(4 * kLoads)));
