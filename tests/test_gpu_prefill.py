@@ -264,3 +264,37 @@ def test_prefill_config4_widths(qa, tmp_path, T):
     finally:
         orc.set_threads(1)
         m.close()
+
+
+def test_prefill_config4_widths_continued(qa, tmp_path):
+    """A 203-token chunk continuing a 1003-key cached context at config-4
+    widths (2 layers, vocabulary 1024, W_gate's scales divided by 4 as
+    above): every query attends 1004..1206 keys, so the attention takes its
+    two-pass form; the steps inside every query of a tile's range take the
+    unmasked path from an unaligned first position, and the last query tile
+    is partial.  Against the oracle's cache fills and last step."""
+    import os
+    P, T = 1003, 203
+    h = qa.QorusHeader(vocab=1024, dim=4096, hidden=14336, n_layers=2, n_heads=32, n_kv=8, max_seq=P + T + 8)
+    path = tmp_path / "c4c.qorus"
+    qa.synthetic.write_synthetic_model(path, h, 79)
+    blob = np.fromfile(path, dtype=np.uint8)
+    lay = qa.model_layout(h)
+    for l in range(h.n_layers):
+        o = lay[f"{l}.w_gate"]
+        g = blob[o: o + h.hidden * (h.dim // 32) * 20].reshape(-1, 20)
+        g[:, 16:] = (g[:, 16:].copy().view(np.float32) * np.float32(0.25)).view(np.uint8)
+    blob.tofile(path)
+    m = qa.Model(path)
+    rng = orc.rng_for(79, 5)
+    kv = np.zeros((h.n_layers, h.n_kv, h.max_seq, 2, 128), np.float32)
+    kv[:, :, :P] = rng.standard_normal((h.n_layers, h.n_kv, P, 2, 128), dtype=np.float32)
+    m.upload_kv(kv)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        toks = [int(t) for t in rng.integers(0, h.vocab, T)]
+        check_prompt(qa, m, h, kv, ref, toks, P, f"{T} tokens at {P}, config-4 widths")
+    finally:
+        orc.set_threads(1)
+        m.close()
