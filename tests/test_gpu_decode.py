@@ -65,6 +65,34 @@ def test_decode_small_gqa(qa, tmp_path):
         m.close()
 
 
+@pytest.mark.parametrize("P", [4100, 9100])
+def test_decode_long_context(qa, tmp_path, P):
+    """Contexts past the config-4 one: 4101 keys (65 score chunks: the
+    chunk-max reduction takes two rounds of 64) and 9101 keys (143 score
+    chunks, 36 P.V chunks: the combine sums its partials in two rounds of
+    32), then greedy steps on the device against the oracle's."""
+    h = qa.QorusHeader(vocab=800, dim=512, hidden=1024, n_layers=2, n_heads=4, n_kv=1, max_seq=P + 16)
+    m, blob, kv = build(qa, tmp_path, h, 17, P)
+    try:
+        ref = orc.DecodeOracle(blob, kv.copy())
+        tok_ref, lg_ref = ref.step(5, P)
+        lg = m.forward([5], P)
+        assert rel_err(lg, lg_ref) <= 1e-4
+        assert int(np.argmax(lg)) == tok_ref
+        kv_gpu = m.download_kv().reshape(kv.shape)
+        for l in range(h.n_layers):
+            assert rel_err(kv_gpu[l, :, P], ref.kv[l, :, P]) <= 1e-4
+        n = 4
+        toks, _ = m.generate(tok_ref, P + 1, n)
+        want, t = [], tok_ref
+        for i in range(n):
+            t, _ = ref.step(t, P + 1 + i)
+            want.append(t)
+        assert toks.tolist() == want
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("n_heads,n_kv,P", [(8, 1, 130), (16, 2, 63), (2, 2, 200)])
 def test_decode_gqa_groups(qa, tmp_path, n_heads, n_kv, P):
     """GQA groups 8 and 1 (the attention kernels are instantiated per group),
