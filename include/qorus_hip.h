@@ -81,7 +81,7 @@ size_t qh_gemv_workspace_bytes(uint32_t N);
  * power-of-two scale per 32-element block (23-24 significant bits for the
  * block maximum); a block where a few outliers set that scale (removing
  * some 6 of its elements would leave less than 3/64 of its maximum) gets a
- * second 23-bit level, so every element within 2^22 of its block maximum
+ * second 23-bit level, so every element within 2^21 of its block maximum
  * is exact.  Measured at the Llama-3 shapes: 0.4-2e-8 with N(0,1) x, and
  * the same with 1..6 equal outliers of 1e3..1e5 per block, or mixed sizes,
  * on zero weights, at or below the reference AVX2 order's error.  A block

@@ -24,7 +24,7 @@
 // Outliers: a block where a few activation outliers set the step (removing
 // some 6 of its elements would leave less than 3/64 of its maximum; the
 // exact rule is in qh_digits.hpp) also gets a second level of digits for
-// the residual x*2^k - x_int, so every element within 2^22 of the block
+// the residual x*2^k - x_int, so every element within 2^21 of the block
 // maximum is represented exactly; the GEMV adds that level's dot, one plane
 // at a time, only in waves whose columns hold such a block (found at the
 // barrier that publishes the digits, or with the digits themselves), in a

@@ -19,7 +19,9 @@ namespace qh {
 //    or infinity (every dot product with the block is then NaN);
 //  * level 2, for "wide" blocks only: the residual B_e = round((x_e * 2^k -
 //    A_e) * 2^23) in 6 more planes.  A + 2^-23 B holds every element within
-//    2^22 of the block maximum exactly.  The planes of a block that is not
+//    2^21 of the block maximum exactly (x * 2^k >= 1 there: the block
+//    maximum lands at 2^21.9 or above; just below, an element can keep 24
+//    bits instead).  The planes of a block that is not
 //    wide are left unwritten; consumers read level 2 only through the flag.
 // A block is wide unless, whichever 6 of its elements are removed, the rest
 // keep a magnitude sum of at least 3/64 of the block maximum (level-1
@@ -54,8 +56,8 @@ constexpr float kLoInv = 1.1920928955078125e-07f;  // 2^-23, the weight of level
 // sum asum = sum_e |A_e| falls below 3 (amax >> 6); block_wide: so do the
 // bounds from c1 = sum_e min(|A_e|, amax >> 4) and c2 = sum_e min(|A_e|,
 // amax >> 6) (needed only when maybe_wide holds).
-__device__ __forceinline__ bool maybe_wide(int amax, int asum) { return asum - 6 * amax < 3 * (amax >> 6); }
-__device__ __forceinline__ bool block_wide(int amax, int c1, int c2) {
+__host__ __device__ __forceinline__ bool maybe_wide(int amax, int asum) { return asum - 6 * amax < 3 * (amax >> 6); }
+__host__ __device__ __forceinline__ bool block_wide(int amax, int c1, int c2) {
     const int t1 = amax >> 4, t2 = amax >> 6;
     return c1 - 6 * t1 < 3 * t2 && c2 - 6 * t2 < 3 * t2;
 }
