@@ -51,6 +51,11 @@ constexpr uint32_t kDigitBias = 8947848u;  // 8 * (16^6 - 1) / 15
 constexpr uint32_t kXdMeta = 6;            // plane index of (k, z, wide, 0)
 constexpr uint32_t kXdLo = 7;              // first level-2 plane
 constexpr float kLoInv = 1.1920928955078125e-07f;  // 2^-23, the weight of level 2
+// A block's integer dot with level-1 (or level-2) digits: 32 products of a
+// weight digit (|q - 8| <= 8) and an integer of at most kDigitMax.
+static_assert(32LL * 8 * kDigitMax < (1LL << 31), "a block's integer dot fits int32");
+static_assert(kDigitMax == 7 * ((1 << 24) - 1) / 15 && kDigitBias == 8u * ((1u << 24) - 1u) / 15u,
+              "6 balanced base-16 digits");
 
 // The wide test, in two stages.  maybe_wide: the bound from the magnitude
 // sum asum = sum_e |A_e| falls below 3 (amax >> 6); block_wide: so do the
